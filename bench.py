@@ -1,0 +1,300 @@
+#!/usr/bin/env python3
+"""Benchmark of the MLA decode hot path on one MI355X.
+
+A step = one decode step of BASELINE.json's headline workload (config 3):
+B=32 sequences x 8192 cached positions, H=128, d_c=512, d_R=64, bf16 latent
+cache, fp32 accumulation, one query token per sequence:
+    q_abs = q_nope . W_UK  ->  split-KV latent attention (MFMA kernel)
+    ->  log-sum-exp combine + W_UV projection.
+All inputs are resident in HBM before timing. The step is launched through the
+C ABI (la_mla_decode) on one stream; HIP events bracket the K timed steps and,
+inside every step, the attention kernel alone (for the roofline line).
+
+Prints ONE JSON line. ``value`` is microseconds per decode step (lower is
+better); ``latent_cache_GBps`` is the whole-step cache read rate; ``roofline``
+is the attention kernel's algorithmic latent-cache bytes (1152 B per sequence
+position, one pass) over its measured duration against 8 TB/s.
+``cpu_baseline`` times this repo's CPU restatement of the reference path
+(oracle/, numpy float32 absorbed math) on a bounded sample of the same
+workload, extrapolated to one step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "latent-attn_amd"))
+sys.path.insert(0, ROOT)
+
+CONFIGS = {
+    # name: (batch, seq_len or None for ragged, description)
+    "cfg2": dict(batch=1, seq_len=8192, desc="DeepSeek-V2 single-sequence decode B=1 S=8192"),
+    "cfg3": dict(batch=32, seq_len=8192, desc="batched uniform decode B=32 S=8192"),
+    "cfg4": dict(batch=64, seq_len=None, desc="ragged decode B=64 len U[512,32768] seed 0"),
+    "cfg5": dict(batch=4, seq_len=131072, desc="long-context decode B=4 S=131072"),
+}
+HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+BYTES_PER_POS = 1152  # (512 + 64) * 2, one pass over the latent cache
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def hip_runtime():
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    return hip
+
+
+def new_event(hip):
+    e = ctypes.c_void_p()
+    assert hip.hipEventCreate(ctypes.byref(e)) == 0
+    return e
+
+
+def elapsed_ms(hip, a, b) -> float:
+    t = ctypes.c_float()
+    assert hip.hipEventElapsedTime(ctypes.byref(t), a, b) == 0
+    return t.value
+
+
+def build_inputs(cfg_name: str, device, seed: int = 0):
+    import numpy as np
+    import torch
+
+    from latent_attn import MLAConfig, build_rope_tables
+
+    spec = CONFIGS[cfg_name]
+    cfg = MLAConfig.deepseek_v2()
+    B = spec["batch"]
+    g = torch.Generator(device=device).manual_seed(seed)
+    row = cfg.kv_lora_rank + cfg.qk_rope_head_dim
+    if spec["seq_len"] is None:
+        lens = np.random.RandomState(seed).randint(512, 32769, B)
+        offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        total = int(offsets[-1])
+        max_len = int(lens.max())
+    else:
+        lens = np.full(B, spec["seq_len"])
+        offsets = None
+        total = B * spec["seq_len"]
+        max_len = spec["seq_len"]
+    kv = torch.randn(total, row, generator=g, device=device, dtype=torch.float32).to(torch.bfloat16)
+    std = 1.0 / math.sqrt(cfg.kv_lora_rank)
+    W_UK = (torch.randn(cfg.num_heads * cfg.qk_nope_head_dim, cfg.kv_lora_rank, generator=g, device=device) * std)
+    W_UV = (torch.randn(cfg.num_heads * cfg.v_head_dim, cfg.kv_lora_rank, generator=g, device=device) * std)
+    W_UK, W_UV = W_UK.to(torch.bfloat16), W_UV.to(torch.bfloat16)
+    q_nope = torch.randn(B, cfg.num_heads, cfg.qk_nope_head_dim, generator=g, device=device)
+    q_rope = torch.randn(B, cfg.num_heads, cfg.qk_rope_head_dim, generator=g, device=device)
+    cos, sin = build_rope_tables(max_len, cfg.qk_rope_head_dim, device=device)
+    off_t = torch.from_numpy(offsets).to(device) if offsets is not None else None
+    return dict(cfg=cfg, B=B, lens=lens, total=total, kv=kv, W_UK=W_UK, W_UV=W_UV, q_nope=q_nope,
+                q_rope=q_rope, cos=cos.contiguous(), sin=sin.contiguous(), offsets=off_t, max_len=max_len,
+                seq_len=spec["seq_len"])
+
+
+def decode_args(inp, out, capi):
+    a = capi.DecodeArgs()
+    a.kv_cache = inp["kv"].data_ptr()
+    a.kv_dtype = capi.LA_DTYPE_BF16
+    a.total_rows = inp["total"]
+    a.num_seqs = inp["B"]
+    if inp["offsets"] is None:
+        a.seq_len = inp["seq_len"]
+    else:
+        a.seq_offsets = inp["offsets"].data_ptr()
+    a.queries_per_seq = 1
+    a.q_nope = inp["q_nope"].data_ptr()
+    a.W_UK = inp["W_UK"].data_ptr()
+    a.w_uk_dtype = capi.LA_DTYPE_BF16
+    a.q_rope = inp["q_rope"].data_ptr()
+    a.W_UV = inp["W_UV"].data_ptr()
+    a.w_uv_dtype = capi.LA_DTYPE_BF16
+    a.rope_cos = inp["cos"].data_ptr()
+    a.rope_sin = inp["sin"].data_ptr()
+    a.rope_rows = inp["cos"].shape[0]
+    a.output = out.data_ptr()
+    a.cfg = capi.config(inp["cfg"])
+    return a
+
+
+def cpu_baseline(inp, budget_s: float = 12.0):
+    """Time the oracle's absorbed float32 path (this repo's CPU restatement of
+    the reference math) on whole sequences of the workload, one at a time,
+    until ~budget_s; extrapolate to one step (all B sequences)."""
+    import numpy as np
+
+    from oracle import mla_oracle as mo
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    cfg = inp["cfg"]
+    d = mo.Dims(cfg.d_model, cfg.kv_lora_rank, cfg.qk_nope_head_dim, cfg.qk_rope_head_dim, cfg.num_heads,
+                cfg.v_head_dim)
+    W_UK = inp["W_UK"].float().cpu().numpy()
+    W_UV = inp["W_UV"].float().cpu().numpy()
+    cos = inp["cos"].cpu().numpy()
+    sin = inp["sin"].cpu().numpy()
+    lens = [int(x) for x in inp["lens"]]
+    offs = np.concatenate([[0], np.cumsum(lens)])
+    done_pos, done_seq, spent = 0, 0, 0.0
+    while spent < budget_s and done_seq < inp["B"]:
+        b = done_seq
+        kv = inp["kv"][offs[b]:offs[b + 1]].float().cpu().numpy()
+        qn = inp["q_nope"][b].cpu().numpy()
+        qr = inp["q_rope"][b].cpu().numpy()
+        t0 = time.perf_counter()
+        qa = mo.absorb_q(qn, W_UK, d, dtype=np.float32)
+        acc, _ = mo.absorbed_latent(kv, qa, qr, cos, sin, d, dtype=np.float32)
+        mo.project_wuv(acc, W_UV, d, dtype=np.float32)
+        spent += time.perf_counter() - t0
+        done_pos += lens[b]
+        done_seq += 1
+    total_pos = int(sum(lens))
+    us_step = spent / done_pos * total_pos * 1e6
+    return {
+        "value": round(us_step, 1),
+        "unit": "us/step",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"{done_seq} of {inp['B']} sequences ({done_pos} positions) through oracle/mla_oracle.py "
+                  f"absorbed float32 path (absorb, latent attention, W_UV), extrapolated by positions",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--variant", type=int, default=0, help="0 auto, 1 VALU kernel, 2 MFMA kernel")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs on a single MI355X "
+              "and has no multi-GPU path.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from latent_attn import capi
+
+    device = torch.device("cuda:0")
+    lib = capi.load()
+    hip = hip_runtime()
+    log(f"[bench] building inputs for {args.config}")
+    inp = build_inputs(args.config, device)
+    cfg = inp["cfg"]
+    B = inp["B"]
+    out = torch.empty(B, cfg.num_heads, cfg.v_head_dim, device=device, dtype=torch.float32)
+    a = decode_args(inp, out, capi)
+    a.kernel_variant = args.variant
+    ws_bytes = lib.la_mla_decode_workspace_size(ctypes.byref(a))
+    assert ws_bytes > 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = ws_bytes
+    stream = torch.cuda.current_stream().cuda_stream
+    torch.cuda.synchronize()
+
+    def step(ev_b=None, ev_e=None):
+        a.decode_event_begin = ev_b
+        a.decode_event_end = ev_e
+        st = lib.la_mla_decode(ctypes.byref(a), ctypes.c_void_p(stream))
+        if st != 0:
+            raise RuntimeError(f"la_mla_decode: {lib.la_status_string(st).decode()} hip={lib.la_last_hip_error()}")
+
+    log(f"[bench] warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    evs = [(new_event(hip), new_event(hip)) for _ in range(K)]
+    t_start, t_end = new_event(hip), new_event(hip)
+    log(f"[bench] timing {K} steps")
+    torch.cuda.synchronize()
+    hip.hipEventRecord(t_start, ctypes.c_void_p(stream))
+    for i in range(K):
+        step(evs[i][0], evs[i][1])
+    hip.hipEventRecord(t_end, ctypes.c_void_p(stream))
+    hip.hipEventSynchronize(t_end)
+    torch.cuda.synchronize()
+    ms_total = elapsed_ms(hip, t_start, t_end)
+    kern_ms = sorted(elapsed_ms(hip, b, e) for b, e in evs)
+    kern_avg = sum(kern_ms) / K
+    ms_step = ms_total / K
+    us_step = ms_step * 1e3
+
+    total_pos = int(inp["total"])
+    cache_bytes = total_pos * BYTES_PER_POS
+    flops_attn = total_pos * 2 * cfg.num_heads * (cfg.kv_lora_rank + cfg.qk_rope_head_dim + cfg.kv_lora_rank)
+    achieved_gbps = cache_bytes / (kern_avg * 1e-3) / 1e9
+    line = {
+        "metric": "\u00b5s/decode step + achieved latent-cache HBM GB/s, H=128 d_c=512, B=32 seq=8K",
+        "value": round(us_step, 2),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": CONFIGS[args.config]["desc"],
+            "batch": B,
+            "seq_len": inp["seq_len"] if inp["seq_len"] else "ragged",
+            "total_positions": total_pos,
+            "num_heads": cfg.num_heads,
+            "kv_lora_rank": cfg.kv_lora_rank,
+            "qk_rope_head_dim": cfg.qk_rope_head_dim,
+            "cache_dtype": "bf16",
+            "accumulate": "fp32",
+            "kernel_variant": args.variant,
+        },
+        "tokens_per_s": round(B / (ms_step * 1e-3), 1),
+        "latent_cache_GBps": round(cache_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "attn_kernel_us": round(kern_avg * 1e3, 2),
+        "attn_kernel_us_p10_p90": [round(kern_ms[K // 10] * 1e3, 2), round(kern_ms[(9 * K) // 10] * 1e3, 2)],
+        "mfma_frac_of_bf16_peak": round(flops_attn / (kern_avg * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+        },
+    }
+    for b, e in evs:
+        hip.hipEventDestroy(b)
+        hip.hipEventDestroy(e)
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline")
+        line["cpu_baseline"] = cpu_baseline(inp)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,176 @@
+/*
+ * latent_attn.h -- C ABI of the MI355X (gfx950) multi-head latent attention
+ * decode library (liblatent_attn_hip.so).
+ *
+ * Plain C: pointers, sizes, integer tags. No torch or HIP types appear in the
+ * signatures; a stream is passed as `void*` (a hipStream_t, NULL = default
+ * stream). Every entry point is asynchronous on that stream, returns an
+ * la_status, and never calls exit(). Device pointers are non-owning.
+ *
+ * Reference interfaces replaced (paths relative to the reference repo):
+ *   la_fused_mla          <- launch_fused_mla          src/fused_mla.cuh:51,
+ *                            src/fused_mla.cu:271-296
+ *   la_batched_fused_mla  <- launch_batched_fused_mla  src/fused_mla_batched.cuh:35,
+ *                            src/fused_mla_batched.cu:109-130
+ *   la_absorb_q           <- host absorption loop tests/test_correctness.cu:29-46
+ *                            and einsum tests/test_python.py:97-99
+ *   la_mla_decode         <- the decode step the north star adds on top of the
+ *                            reference API (per-sequence / ragged caches, split-KV
+ *                            with log-sum-exp combine, fused W_UV projection)
+ *   la_mla_config         <- MLAConfig                 src/mla_config.cuh:7-13
+ *                            (same six ints in the same order)
+ *
+ * Layouts (all row-major, contiguous):
+ *   latent cache row   [c_t (kv_lora_rank) | k_rope (qk_rope_head_dim)]
+ *                      (src/mla_config.cuh:43-48)
+ *   W_UK               (num_heads*qk_nope_head_dim, kv_lora_rank)
+ *   W_UV               (num_heads*v_head_dim, kv_lora_rank); head h owns rows
+ *                      [h*v_head_dim, (h+1)*v_head_dim)   (src/fused_mla.cu:258-267)
+ *   rope_cos/rope_sin  (rows >= longest sequence, qk_rope_head_dim/2) float32,
+ *                      indexed by the key's position inside its sequence;
+ *                      rotate-half pairing (i, i + d_R/2)   (src/fused_mla.cu:34-54)
+ *   q_rope             already rotated for the query position (the reference
+ *                      never rotates q; src/fused_mla.cu:34-54)
+ *   scale              1/sqrt(qk_nope_head_dim + qk_rope_head_dim), applied
+ *                      inside (src/fused_mla.cu:284)
+ *   outputs            float32 (.., num_heads, v_head_dim)
+ *
+ * An empty sequence (length 0) produces a zero output row (the reference's
+ * kernel would divide by zero there; its PyTorch reference sums an empty set).
+ */
+#ifndef LATENT_ATTN_H
+#define LATENT_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LA_ABI_VERSION 1
+
+typedef enum la_status {
+  LA_SUCCESS = 0,
+  LA_ERROR_INVALID_VALUE = 1, /* null pointer, bad shape or config         */
+  LA_ERROR_NOT_SUPPORTED = 2, /* no kernel for this dtype / dims / device   */
+  LA_ERROR_WORKSPACE = 3,     /* caller workspace smaller than required     */
+  LA_ERROR_HIP = 4            /* a HIP call failed: see la_last_hip_error() */
+} la_status;
+
+typedef enum la_dtype {
+  LA_DTYPE_F32 = 0,
+  LA_DTYPE_F16 = 1,
+  LA_DTYPE_BF16 = 2
+} la_dtype;
+
+/* Same fields and order as the reference MLAConfig (src/mla_config.cuh:7-13). */
+typedef struct la_mla_config {
+  int32_t d_model;
+  int32_t kv_lora_rank;     /* d_c */
+  int32_t qk_nope_head_dim; /* d_n */
+  int32_t qk_rope_head_dim; /* d_R */
+  int32_t num_heads;
+  int32_t v_head_dim;
+} la_mla_config;
+
+/* Arguments of one decode step (la_mla_decode). */
+typedef struct la_decode_args {
+  /* packed latent cache: total_rows rows of (kv_lora_rank + qk_rope_head_dim) */
+  const void* kv_cache;
+  int32_t kv_dtype; /* la_dtype */
+  int64_t total_rows;
+  /* sequences: num_seqs caches inside kv_cache.
+   * seq_offsets == NULL: sequence s owns rows [s*seq_len, (s+1)*seq_len).
+   * otherwise seq_offsets is a DEVICE int32 array of num_seqs+1 non-decreasing
+   * row offsets with seq_offsets[num_seqs] <= total_rows. */
+  int32_t num_seqs;
+  int32_t seq_len;
+  const int32_t* seq_offsets;
+  /* query tokens sharing each sequence's cache (1 for ordinary decode; the
+   * reference's shared-cache batched form is num_seqs = 1, queries_per_seq = B).
+   * Query token t = s*queries_per_seq + j. */
+  int32_t queries_per_seq;
+  /* queries: either q_nope (+ W_UK, absorbed inside) or q_absorbed.
+   * q_nope (tokens, num_heads, qk_nope_head_dim) f32; W_UK see header comment.
+   * q_absorbed (tokens, num_heads, kv_lora_rank) f32. Exactly one of q_nope /
+   * q_absorbed must be non-NULL. */
+  const float* q_nope;
+  const void* W_UK;
+  int32_t w_uk_dtype;
+  const float* q_absorbed;
+  const float* q_rope; /* (tokens, num_heads, qk_rope_head_dim) f32 */
+  const void* W_UV;
+  int32_t w_uv_dtype;
+  const float* rope_cos;
+  const float* rope_sin;
+  /* rows in rope_cos / rope_sin; 0 = unchecked (caller guarantees at least
+   * the longest sequence). Positions past it read the last row instead of
+   * faulting. */
+  int64_t rope_rows;
+  float* output; /* (tokens, num_heads, v_head_dim) f32 */
+  la_mla_config cfg;
+  /* scratch for split partials (and the absorbed query when q_nope is given).
+   * NULL: the library takes stream-ordered memory (hipMallocAsync) and returns
+   * it on the same stream. */
+  void* workspace;
+  size_t workspace_bytes;
+  /* tuning / test overrides, 0 = automatic:
+   * chunk_rows     rows per split-KV chunk
+   * kernel_variant 1 = VALU kernel, 2 = MFMA kernel (LA_ERROR_NOT_SUPPORTED if
+   *                the shape has none) */
+  int32_t chunk_rows;
+  int32_t kernel_variant;
+  /* optional hipEvent_t handles recorded on `stream` right before and right
+   * after the split-KV attention kernel (profiling); NULL = not recorded. */
+  void* decode_event_begin;
+  void* decode_event_end;
+} la_decode_args;
+
+/* Human-readable name of an la_status value. */
+const char* la_status_string(int status);
+
+/* Last hipError_t recorded by a failing call on this host thread (0 = none). */
+int la_last_hip_error(void);
+
+/* Library ABI version (LA_ABI_VERSION). */
+int la_abi_version(void);
+
+/* Bytes of workspace la_mla_decode needs for these arguments on the current
+ * device (the fields kv_cache/q/output pointers are not read). */
+size_t la_mla_decode_workspace_size(const la_decode_args* args);
+
+/* One decode step: [absorb] -> split-KV latent attention -> log-sum-exp
+ * combine -> W_UV projection. */
+int la_mla_decode(const la_decode_args* args, void* stream);
+
+/* Drop-in for launch_fused_mla (src/fused_mla.cuh:51): one query token over
+ * one cache of seq_len rows. kv_cache / W_UV dtypes: F16 (the reference
+ * contract), BF16 or F32. */
+int la_fused_mla(const void* kv_cache, int kv_dtype, int seq_len, const float* q_absorbed, const float* q_rope,
+                 const void* W_UV, int w_uv_dtype, const float* rope_cos, const float* rope_sin, float* output,
+                 const la_mla_config* cfg, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Drop-in for launch_batched_fused_mla (src/fused_mla_batched.cuh:35):
+ * batch_size query tokens over one SHARED cache. q_absorbed (B, nh, dc),
+ * q_rope (B, nh, dR), output (B, nh, dv). */
+int la_batched_fused_mla(const void* kv_cache, int kv_dtype, int seq_len, int batch_size, const float* q_absorbed,
+                         const float* q_rope, const void* W_UV, int w_uv_dtype, const float* rope_cos,
+                         const float* rope_sin, float* output, const la_mla_config* cfg, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* Workspace bytes la_fused_mla / la_batched_fused_mla need (batch_size 1 for
+ * la_fused_mla). */
+size_t la_fused_mla_workspace_size(int seq_len, int batch_size, const la_mla_config* cfg);
+
+/* Query absorption q_abs[t,h,c] = sum_i q_nope[t,h,i] * W_UK[h*dn+i, c]
+ * (tests/test_correctness.cu:29-46). q_nope (tokens, nh, dn) f32,
+ * q_absorbed (tokens, nh, dc) f32. */
+int la_absorb_q(const float* q_nope, const void* W_UK, int w_uk_dtype, float* q_absorbed, int tokens,
+                const la_mla_config* cfg, void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* LATENT_ATTN_H */

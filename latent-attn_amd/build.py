@@ -1,0 +1,109 @@
+"""Build the in-tree native artefacts of the latent_attn package.
+
+* ``latent_attn/liblatent_attn_hip.so`` -- the HIP kernels and the C ABI of
+  include/latent_attn.h, compiled for gfx950 with hipcc (one object per
+  source, compiled in parallel, then linked).
+* ``latent_attn/_C<ext>`` -- the PyTorch-ROCm extension (pybind11) that wraps
+  the C ABI; host-only C++ compiled with g++ against torch's headers and
+  linked to the library with an $ORIGIN rpath.
+
+Usage: ``python latent-attn_amd/build.py [--lib-only]``. Always recompiles.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import subprocess
+import sys
+import sysconfig
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+PKG = os.path.join(HERE, "latent_attn")
+INC = os.path.join(ROOT, "include")
+BUILD = os.path.join(ROOT, "_build")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+
+LIB_NAME = "liblatent_attn_hip.so"
+HIP_SOURCES = ["la_capi.hip", "la_generic.hip", "la_mfma.hip"]
+
+# -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32.
+HIP_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INC}",
+    f"-I{CSRC}",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in res.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if res.returncode != 0:
+        sys.stderr.write(out + "\n")
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}")
+
+
+def build_lib(jobs: int = 8) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    objs = []
+    cmds = []
+    for src in HIP_SOURCES:
+        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        objs.append(obj)
+        cmds.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(cmds)))) as ex:
+        list(ex.map(_run, cmds))
+    out = os.path.join(PKG, LIB_NAME)
+    tmp = out + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
+    os.replace(tmp, out)
+    return out
+
+
+def build_ext() -> str:
+    import torch
+    from torch.utils import cpp_extension
+
+    suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+    out = os.path.join(PKG, "_C" + suffix)
+    obj = os.path.join(BUILD, "bindings.o")
+    os.makedirs(BUILD, exist_ok=True)
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    incs = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"], os.path.join(ROCM, "include"), INC]
+    cflags = [
+        "-O2", "-std=c++17", "-fPIC", "-w",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        "-DTORCH_EXTENSION_NAME=_C", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        *[f"-I{i}" for i in incs],
+    ]
+    _run(["g++", *cflags, "-c", os.path.join(CSRC, "bindings.cpp"), "-o", obj])
+    torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    tmp = out + ".tmp"
+    _run([
+        "g++", "-shared", "-o", tmp, obj,
+        f"-L{PKG}", "-llatent_attn_hip",
+        f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+        f"-L{os.path.join(ROCM, 'lib')}", "-lamdhip64",
+        "-Wl,-rpath,$ORIGIN",
+    ])
+    os.replace(tmp, out)
+    return out
+
+
+def build(lib_only: bool = False) -> None:
+    build_lib()
+    if not lib_only:
+        build_ext()
+
+
+if __name__ == "__main__":
+    build(lib_only="--lib-only" in sys.argv)
+    print("built", os.path.join(PKG, LIB_NAME))

@@ -1,0 +1,320 @@
+// latent_attn._C -- PyTorch-ROCm extension over the C ABI of
+// liblatent_attn_hip.so (include/latent_attn.h).
+//
+// Mirrors the reference bindings (csrc/bindings.cpp:249-256 in the reference
+// repo): same function names, argument order, shape checks and error
+// messages, output allocated as float32 on kv_cache's device, launched on the
+// current stream. Differences: the 16-bit dtype may be float16 (reference
+// contract) or bfloat16, float32 caches/weights select the fp32 path, a
+// device guard is taken, and two functions are added (mla_decode_forward,
+// absorb_q_forward). No tensor math happens here; all compute is in the HIP
+// library.
+#include <torch/extension.h>
+#include <c10/hip/HIPStream.h>
+
+#include <stdexcept>
+#include <string>
+
+#include "latent_attn.h"
+
+namespace {
+
+// MLAConfig::validate (src/mla_config.cuh:35-40): std::invalid_argument.
+la_mla_config config_from_args(int d_model, int kv_lora_rank, int qk_nope_head_dim, int qk_rope_head_dim,
+                               int num_heads, int v_head_dim) {
+  la_mla_config c{d_model, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, num_heads, v_head_dim};
+  if (kv_lora_rank <= 0 || qk_nope_head_dim <= 0 || qk_rope_head_dim <= 0)
+    throw std::invalid_argument("MLA dims must be positive");
+  if (num_heads <= 0 || v_head_dim <= 0) throw std::invalid_argument("num_heads and v_head_dim must be positive");
+  if (qk_rope_head_dim % 2 != 0) throw std::invalid_argument("qk_rope_head_dim must be even (rotate-half RoPE)");
+  return c;
+}
+
+int dtype_tag(const torch::Tensor& t) {
+  switch (t.scalar_type()) {
+    case torch::kFloat32: return LA_DTYPE_F32;
+    case torch::kFloat16: return LA_DTYPE_F16;
+    case torch::kBFloat16: return LA_DTYPE_BF16;
+    default: return -1;
+  }
+}
+
+void check_storage(const torch::Tensor& t, const char* name) {
+  TORCH_CHECK(dtype_tag(t) >= 0, name, " must be float16, bfloat16 or float32, got ", t.dtype());
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+  TORCH_CHECK(t.is_cuda(), name, " must be on CUDA");
+}
+
+void check_fp32_contiguous(const torch::Tensor& t, const char* name) {
+  TORCH_CHECK(t.dtype() == torch::kFloat32, name, " must be float32, got ", t.dtype());
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+  TORCH_CHECK(t.is_cuda(), name, " must be on CUDA");
+}
+
+void check_same_device(const torch::Tensor& ref, const torch::Tensor& t, const char* name) {
+  TORCH_CHECK(t.device() == ref.device(), name, " must be on the same device as kv_cache");
+}
+
+void check_rope(const torch::Tensor& cos, const torch::Tensor& sin, int64_t rows, const la_mla_config& c) {
+  TORCH_CHECK(cos.dim() == 2 && sin.dim() == 2, "rope_cos / rope_sin must be 2D (seq_len, qk_rope_head_dim/2)");
+  TORCH_CHECK(cos.size(1) == c.qk_rope_head_dim / 2 && sin.size(1) == c.qk_rope_head_dim / 2,
+              "rope_cos / rope_sin dim1 must be ", c.qk_rope_head_dim / 2);
+  TORCH_CHECK(cos.size(0) >= rows && sin.size(0) >= rows, "rope_cos / rope_sin need at least ", rows, " rows");
+}
+
+void check_status(int st, const char* what) {
+  if (st == LA_SUCCESS) return;
+  std::string msg = std::string(what) + " failed: " + la_status_string(st);
+  if (st == LA_ERROR_HIP) msg += std::string(" (") + hipGetErrorString((hipError_t)la_last_hip_error()) + ")";
+  TORCH_CHECK(false, msg);
+}
+
+torch::Tensor workspace(const torch::Tensor& like, size_t bytes) {
+  return torch::empty({(int64_t)std::max<size_t>(bytes, 1)}, like.options().dtype(torch::kUInt8));
+}
+
+void* current_stream() { return (void*)c10::hip::getCurrentHIPStream().stream(); }
+
+}  // namespace
+
+// fused_mla_forward -- reference csrc/bindings.cpp:126-176
+//   kv_cache (seq_len, dc+dR); q_absorbed (nh, dc) f32; q_rope (nh, dR) f32;
+//   W_UV (nh*dv, dc); rope tables (>= seq_len, dR/2) f32 -> (nh, dv) f32
+torch::Tensor fused_mla_forward(torch::Tensor kv_cache, torch::Tensor q_absorbed, torch::Tensor q_rope,
+                                torch::Tensor W_UV, torch::Tensor rope_cos, torch::Tensor rope_sin, int d_model,
+                                int kv_lora_rank, int qk_nope_head_dim, int qk_rope_head_dim, int num_heads,
+                                int v_head_dim) {
+  check_storage(kv_cache, "kv_cache");
+  check_fp32_contiguous(q_absorbed, "q_absorbed");
+  check_fp32_contiguous(q_rope, "q_rope");
+  check_storage(W_UV, "W_UV");
+  check_fp32_contiguous(rope_cos, "rope_cos");
+  check_fp32_contiguous(rope_sin, "rope_sin");
+  la_mla_config cfg =
+      config_from_args(d_model, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, num_heads, v_head_dim);
+
+  TORCH_CHECK(kv_cache.dim() == 2, "kv_cache must be 2D (seq_len, kv_lora_rank + qk_rope_head_dim)");
+  const int64_t seq_len = kv_cache.size(0);
+  TORCH_CHECK(kv_cache.size(1) == kv_lora_rank + qk_rope_head_dim, "kv_cache dim1 mismatch");
+  TORCH_CHECK(q_absorbed.dim() == 2 && q_absorbed.size(0) == num_heads && q_absorbed.size(1) == kv_lora_rank,
+              "q_absorbed shape mismatch");
+  TORCH_CHECK(q_rope.dim() == 2 && q_rope.size(0) == num_heads && q_rope.size(1) == qk_rope_head_dim,
+              "q_rope shape mismatch");
+  TORCH_CHECK(W_UV.dim() == 2 && W_UV.size(0) == (int64_t)num_heads * v_head_dim && W_UV.size(1) == kv_lora_rank,
+              "W_UV shape mismatch");
+  check_rope(rope_cos, rope_sin, seq_len, cfg);
+  for (auto* t : {&q_absorbed, &q_rope, &W_UV, &rope_cos, &rope_sin}) check_same_device(kv_cache, *t, "inputs");
+  TORCH_CHECK(seq_len <= INT32_MAX, "seq_len too large");
+
+  const at::DeviceGuard guard(kv_cache.device());
+  auto output = torch::empty({num_heads, v_head_dim}, kv_cache.options().dtype(torch::kFloat32));
+  const size_t ws_bytes = la_fused_mla_workspace_size((int)seq_len, 1, &cfg);
+  auto ws = workspace(kv_cache, ws_bytes);
+  int st = la_fused_mla(kv_cache.data_ptr(), dtype_tag(kv_cache), (int)seq_len, q_absorbed.data_ptr<float>(),
+                        q_rope.data_ptr<float>(), W_UV.data_ptr(), dtype_tag(W_UV), rope_cos.data_ptr<float>(),
+                        rope_sin.data_ptr<float>(), output.data_ptr<float>(), &cfg, ws.data_ptr(), ws_bytes,
+                        current_stream());
+  check_status(st, "launch_fused_mla");
+  return output;
+}
+
+// batched_fused_mla_forward -- reference csrc/bindings.cpp:188-244
+//   B query tokens over one shared cache -> (B, nh, dv) f32
+torch::Tensor batched_fused_mla_forward(torch::Tensor kv_cache, torch::Tensor q_absorbed, torch::Tensor q_rope,
+                                        torch::Tensor W_UV, torch::Tensor rope_cos, torch::Tensor rope_sin,
+                                        int d_model, int kv_lora_rank, int qk_nope_head_dim, int qk_rope_head_dim,
+                                        int num_heads, int v_head_dim) {
+  check_storage(kv_cache, "kv_cache");
+  check_fp32_contiguous(q_absorbed, "q_absorbed");
+  check_fp32_contiguous(q_rope, "q_rope");
+  check_storage(W_UV, "W_UV");
+  check_fp32_contiguous(rope_cos, "rope_cos");
+  check_fp32_contiguous(rope_sin, "rope_sin");
+  la_mla_config cfg =
+      config_from_args(d_model, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, num_heads, v_head_dim);
+
+  TORCH_CHECK(q_absorbed.dim() == 3, "q_absorbed must be 3D (batch, num_heads, kv_lora_rank)");
+  TORCH_CHECK(q_rope.dim() == 3, "q_rope must be 3D (batch, num_heads, qk_rope_head_dim)");
+  const int64_t batch = q_absorbed.size(0);
+  TORCH_CHECK(kv_cache.dim() == 2, "kv_cache must be 2D (seq_len, kv_lora_rank + qk_rope_head_dim)");
+  const int64_t seq_len = kv_cache.size(0);
+  TORCH_CHECK(batch > 0, "batch_size must be positive, got ", batch);
+  TORCH_CHECK(q_rope.size(0) == batch, "q_rope batch dim must match q_absorbed batch dim: ", q_rope.size(0), " vs ",
+              batch);
+  TORCH_CHECK(q_absorbed.size(1) == num_heads && q_absorbed.size(2) == kv_lora_rank,
+              "q_absorbed shape mismatch: expected (", batch, ", ", num_heads, ", ", kv_lora_rank, ") got (",
+              q_absorbed.size(0), ", ", q_absorbed.size(1), ", ", q_absorbed.size(2), ")");
+  TORCH_CHECK(q_rope.size(1) == num_heads && q_rope.size(2) == qk_rope_head_dim, "q_rope shape mismatch");
+  TORCH_CHECK(kv_cache.size(1) == kv_lora_rank + qk_rope_head_dim, "kv_cache dim1 mismatch");
+  TORCH_CHECK(W_UV.dim() == 2 && W_UV.size(0) == (int64_t)num_heads * v_head_dim && W_UV.size(1) == kv_lora_rank,
+              "W_UV shape mismatch");
+  check_rope(rope_cos, rope_sin, seq_len, cfg);
+  for (auto* t : {&q_absorbed, &q_rope, &W_UV, &rope_cos, &rope_sin}) check_same_device(kv_cache, *t, "inputs");
+  TORCH_CHECK(seq_len <= INT32_MAX && batch <= INT32_MAX / num_heads, "problem too large");
+
+  const at::DeviceGuard guard(kv_cache.device());
+  auto output = torch::empty({batch, num_heads, v_head_dim}, kv_cache.options().dtype(torch::kFloat32));
+  const size_t ws_bytes = la_fused_mla_workspace_size((int)seq_len, (int)batch, &cfg);
+  auto ws = workspace(kv_cache, ws_bytes);
+  int st = la_batched_fused_mla(kv_cache.data_ptr(), dtype_tag(kv_cache), (int)seq_len, (int)batch,
+                                q_absorbed.data_ptr<float>(), q_rope.data_ptr<float>(), W_UV.data_ptr(),
+                                dtype_tag(W_UV), rope_cos.data_ptr<float>(), rope_sin.data_ptr<float>(),
+                                output.data_ptr<float>(), &cfg, ws.data_ptr(), ws_bytes, current_stream());
+  check_status(st, "launch_batched_fused_mla");
+  return output;
+}
+
+// mla_decode_forward -- the full decode step the north star adds: per-sequence
+// caches, query absorption inside, split-KV + log-sum-exp combine, W_UV.
+//   kv_cache: (B, S, dc+dR) uniform, or (T, dc+dR) packed with seq_offsets
+//   seq_offsets: None or int32 (B+1,) device tensor of row offsets
+//   q_nope (B, nh, dn) f32; q_rope (B, nh, dR) f32 (already rotated)
+//   W_UK (nh*dn, dc); W_UV (nh*dv, dc); rope tables (>= longest seq, dR/2)
+//   returns (B, nh, dv) f32. chunk_rows / kernel_variant: tuning overrides.
+torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, torch::Tensor q_rope,
+                                 torch::Tensor W_UK, torch::Tensor W_UV, torch::Tensor rope_cos,
+                                 torch::Tensor rope_sin, c10::optional<torch::Tensor> seq_offsets, int d_model,
+                                 int kv_lora_rank, int qk_nope_head_dim, int qk_rope_head_dim, int num_heads,
+                                 int v_head_dim, int chunk_rows, int kernel_variant) {
+  check_storage(kv_cache, "kv_cache");
+  check_fp32_contiguous(q_nope, "q_nope");
+  check_fp32_contiguous(q_rope, "q_rope");
+  check_storage(W_UK, "W_UK");
+  check_storage(W_UV, "W_UV");
+  check_fp32_contiguous(rope_cos, "rope_cos");
+  check_fp32_contiguous(rope_sin, "rope_sin");
+  la_mla_config cfg =
+      config_from_args(d_model, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, num_heads, v_head_dim);
+  const int64_t row = kv_lora_rank + qk_rope_head_dim;
+  TORCH_CHECK(q_nope.dim() == 3 && q_nope.size(1) == num_heads && q_nope.size(2) == qk_nope_head_dim,
+              "q_nope must be (batch, num_heads, qk_nope_head_dim)");
+  const int64_t batch = q_nope.size(0);
+  TORCH_CHECK(q_rope.dim() == 3 && q_rope.size(0) == batch && q_rope.size(1) == num_heads &&
+                  q_rope.size(2) == qk_rope_head_dim,
+              "q_rope must be (batch, num_heads, qk_rope_head_dim)");
+  TORCH_CHECK(W_UK.dim() == 2 && W_UK.size(0) == (int64_t)num_heads * qk_nope_head_dim && W_UK.size(1) == kv_lora_rank,
+              "W_UK shape mismatch");
+  TORCH_CHECK(W_UV.dim() == 2 && W_UV.size(0) == (int64_t)num_heads * v_head_dim && W_UV.size(1) == kv_lora_rank,
+              "W_UV shape mismatch");
+  TORCH_CHECK(batch <= INT32_MAX / num_heads, "batch too large");
+
+  la_decode_args a{};
+  a.kv_cache = kv_cache.data_ptr();
+  a.kv_dtype = dtype_tag(kv_cache);
+  a.num_seqs = (int32_t)batch;
+  a.queries_per_seq = 1;
+  int64_t longest = 0;
+  if (seq_offsets.has_value() && seq_offsets->defined()) {
+    const auto& off = *seq_offsets;
+    TORCH_CHECK(off.dtype() == torch::kInt32 && off.is_contiguous() && off.is_cuda(),
+                "seq_offsets must be a contiguous int32 CUDA tensor");
+    TORCH_CHECK(off.dim() == 1 && off.size(0) == batch + 1, "seq_offsets must have batch + 1 entries");
+    check_same_device(kv_cache, off, "seq_offsets");
+    TORCH_CHECK(kv_cache.dim() == 2 && kv_cache.size(1) == row, "packed kv_cache must be (total_rows, ", row, ")");
+    a.total_rows = kv_cache.size(0);
+    a.seq_offsets = off.data_ptr<int32_t>();
+    // Sequences are at most total_rows long; positions past the table clamp.
+    longest = 0;
+    a.rope_rows = rope_cos.size(0);
+  } else {
+    TORCH_CHECK(kv_cache.dim() == 3 && kv_cache.size(0) == batch && kv_cache.size(2) == row,
+                "kv_cache must be (batch, seq_len, ", row, ") when seq_offsets is None");
+    TORCH_CHECK(kv_cache.size(1) <= INT32_MAX, "seq_len too large");
+    a.seq_len = (int32_t)kv_cache.size(1);
+    a.total_rows = batch * kv_cache.size(1);
+    longest = kv_cache.size(1);
+    a.rope_rows = rope_cos.size(0);
+  }
+  check_rope(rope_cos, rope_sin, longest, cfg);
+  for (auto* t : {&q_nope, &q_rope, &W_UK, &W_UV, &rope_cos, &rope_sin}) check_same_device(kv_cache, *t, "inputs");
+  a.q_nope = q_nope.data_ptr<float>();
+  a.W_UK = W_UK.data_ptr();
+  a.w_uk_dtype = dtype_tag(W_UK);
+  a.q_rope = q_rope.data_ptr<float>();
+  a.W_UV = W_UV.data_ptr();
+  a.w_uv_dtype = dtype_tag(W_UV);
+  a.rope_cos = rope_cos.data_ptr<float>();
+  a.rope_sin = rope_sin.data_ptr<float>();
+  a.cfg = cfg;
+  a.chunk_rows = chunk_rows;
+  a.kernel_variant = kernel_variant;
+
+  const at::DeviceGuard guard(kv_cache.device());
+  auto output = torch::empty({batch, num_heads, v_head_dim}, kv_cache.options().dtype(torch::kFloat32));
+  a.output = output.data_ptr<float>();
+  const size_t ws_bytes = la_mla_decode_workspace_size(&a);
+  TORCH_CHECK(ws_bytes > 0 || batch == 0, "mla_decode: unsupported arguments");
+  auto ws = workspace(kv_cache, ws_bytes);
+  a.workspace = ws.data_ptr();
+  a.workspace_bytes = ws_bytes;
+  check_status(la_mla_decode(&a, current_stream()), "la_mla_decode");
+  return output;
+}
+
+// absorb_q_forward -- q_abs[t,h,c] = sum_i q_nope[t,h,i] W_UK[h*dn+i, c]
+// (reference tests/test_correctness.cu:29-46, tests/test_python.py:97-99).
+torch::Tensor absorb_q_forward(torch::Tensor q_nope, torch::Tensor W_UK, int d_model, int kv_lora_rank,
+                               int qk_nope_head_dim, int qk_rope_head_dim, int num_heads, int v_head_dim) {
+  check_fp32_contiguous(q_nope, "q_nope");
+  check_storage(W_UK, "W_UK");
+  la_mla_config cfg =
+      config_from_args(d_model, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, num_heads, v_head_dim);
+  TORCH_CHECK(q_nope.dim() >= 2 && q_nope.size(-1) == qk_nope_head_dim && q_nope.size(-2) == num_heads,
+              "q_nope must be (..., num_heads, qk_nope_head_dim)");
+  TORCH_CHECK(W_UK.dim() == 2 && W_UK.size(0) == (int64_t)num_heads * qk_nope_head_dim && W_UK.size(1) == kv_lora_rank,
+              "W_UK shape mismatch");
+  check_same_device(q_nope, W_UK, "W_UK");
+  const int64_t tokens = q_nope.numel() / ((int64_t)num_heads * qk_nope_head_dim);
+  TORCH_CHECK(tokens <= INT32_MAX, "too many tokens");
+  auto sizes = q_nope.sizes().vec();
+  sizes.back() = kv_lora_rank;
+  const at::DeviceGuard guard(q_nope.device());
+  auto out = torch::empty(sizes, q_nope.options());
+  check_status(la_absorb_q(q_nope.data_ptr<float>(), W_UK.data_ptr(), dtype_tag(W_UK), out.data_ptr<float>(),
+                           (int)tokens, &cfg, current_stream()),
+               "la_absorb_q");
+  return out;
+}
+
+// naive_mla_forward -- reference csrc/bindings.cpp:53-114 signature. The
+// result is the same function of the inputs (decompress-then-attend equals
+// absorb-then-attend); it is computed by absorbing q_nope with W_UK on the GPU
+// and running the fused decode, so no (S, nh*dn) K/V is materialised.
+torch::Tensor naive_mla_forward(torch::Tensor kv_cache, torch::Tensor W_UK, torch::Tensor W_UV,
+                                torch::Tensor q_nope, torch::Tensor q_rope, torch::Tensor rope_cos,
+                                torch::Tensor rope_sin, int d_model, int kv_lora_rank, int qk_nope_head_dim,
+                                int qk_rope_head_dim, int num_heads, int v_head_dim) {
+  check_storage(kv_cache, "kv_cache");
+  check_storage(W_UK, "W_UK");
+  check_storage(W_UV, "W_UV");
+  check_fp32_contiguous(q_nope, "q_nope");
+  check_fp32_contiguous(q_rope, "q_rope");
+  check_fp32_contiguous(rope_cos, "rope_cos");
+  check_fp32_contiguous(rope_sin, "rope_sin");
+  config_from_args(d_model, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, num_heads, v_head_dim);
+  TORCH_CHECK(kv_cache.dim() == 2 && kv_cache.size(1) == kv_lora_rank + qk_rope_head_dim, "kv_cache dim1 must be ",
+              kv_lora_rank + qk_rope_head_dim);
+  TORCH_CHECK(q_nope.dim() == 2 && q_nope.size(0) == num_heads && q_nope.size(1) == qk_nope_head_dim,
+              "q_nope shape mismatch");
+  TORCH_CHECK(q_rope.dim() == 2 && q_rope.size(0) == num_heads && q_rope.size(1) == qk_rope_head_dim,
+              "q_rope shape mismatch");
+  auto out = mla_decode_forward(kv_cache.unsqueeze(0), q_nope.unsqueeze(0), q_rope.unsqueeze(0), W_UK, W_UV,
+                                rope_cos, rope_sin, c10::nullopt, d_model, kv_lora_rank, qk_nope_head_dim,
+                                qk_rope_head_dim, num_heads, v_head_dim, 0, 0);
+  return out.squeeze(0);
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("naive_mla_forward", &naive_mla_forward, "MLA forward from q_nope and W_UK (decompress-then-attend result)");
+  m.def("fused_mla_forward", &fused_mla_forward,
+        "Fused absorbed MLA forward (single token, online softmax in latent space)");
+  m.def("batched_fused_mla_forward", &batched_fused_mla_forward,
+        "Batched fused MLA forward (batch tokens, shared KV cache)");
+  m.def("mla_decode_forward", &mla_decode_forward,
+        "Batched MLA decode step over per-sequence or ragged caches (absorb, split-KV, combine, W_UV)",
+        py::arg("kv_cache"), py::arg("q_nope"), py::arg("q_rope"), py::arg("W_UK"), py::arg("W_UV"),
+        py::arg("rope_cos"), py::arg("rope_sin"), py::arg("seq_offsets"), py::arg("d_model"),
+        py::arg("kv_lora_rank"), py::arg("qk_nope_head_dim"), py::arg("qk_rope_head_dim"), py::arg("num_heads"),
+        py::arg("v_head_dim"), py::arg("chunk_rows") = 0, py::arg("kernel_variant") = 0);
+  m.def("absorb_q_forward", &absorb_q_forward, "q_absorbed = q_nope . W_UK per head");
+}

@@ -1,0 +1,309 @@
+// extern "C" entry points of liblatent_attn_hip.so (declared in
+// include/latent_attn.h): argument checking, split-KV planning, workspace
+// carving and kernel dispatch. Host code only; the kernels live in
+// la_generic.hip and la_mfma.hip.
+#include "la_internal.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <mutex>
+#include <vector>
+
+namespace la {
+namespace {
+
+thread_local int g_last_hip_error = 0;
+
+int record_hip(hipError_t e) {
+  g_last_hip_error = (int)e;
+  return LA_ERROR_HIP;
+}
+
+bool valid_dtype(int d) { return d == LA_DTYPE_F32 || d == LA_DTYPE_F16 || d == LA_DTYPE_BF16; }
+
+// Same conditions as MLAConfig::validate (src/mla_config.cuh:35-40) plus the
+// rotate-half requirement of an even rope dimension.
+bool valid_cfg(const la_mla_config* c) {
+  if (!c) return false;
+  if (c->kv_lora_rank <= 0 || c->qk_nope_head_dim <= 0 || c->qk_rope_head_dim <= 0) return false;
+  if (c->num_heads <= 0 || c->v_head_dim <= 0) return false;
+  return (c->qk_rope_head_dim % 2) == 0;
+}
+
+int cu_count() {
+  static std::mutex mu;
+  static std::vector<int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)cache.size() <= dev) cache.resize(dev + 1, 0);
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+enum Variant { kAuto = 0, kGeneric = 1, kMfma = 2 };
+
+struct Plan {
+  bool mfma = false;
+  int chunk_len = 0;
+  int num_chunks = 0;
+  int num_slots = 0;
+  size_t q_abs_off = 0, part_o_off = 0, part_lse_off = 0, total = 0;
+};
+
+// Fills the problem (without workspace pointers) and the plan. The args'
+// chunk_rows / kernel_variant fields are tuning overrides (0 = automatic).
+int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
+  if (!a || !valid_cfg(&a->cfg)) return LA_ERROR_INVALID_VALUE;
+  const int chunk_rows = a->chunk_rows;
+  const int variant = a->kernel_variant;
+  if (chunk_rows < 0 || variant < kAuto || variant > kMfma || a->rope_rows < 0) return LA_ERROR_INVALID_VALUE;
+  if (a->num_seqs < 0 || a->queries_per_seq < 1 || a->total_rows < 0) return LA_ERROR_INVALID_VALUE;
+  if (!valid_dtype(a->kv_dtype) || !valid_dtype(a->w_uv_dtype)) return LA_ERROR_INVALID_VALUE;
+  if (!a->seq_offsets && (a->seq_len < 0 || (int64_t)a->num_seqs * a->seq_len > a->total_rows))
+    return LA_ERROR_INVALID_VALUE;
+  const bool absorb = a->q_nope != nullptr;
+  if (absorb == (a->q_absorbed != nullptr)) return LA_ERROR_INVALID_VALUE;
+  if (absorb && (!a->W_UK || !valid_dtype(a->w_uk_dtype))) return LA_ERROR_INVALID_VALUE;
+  const la_mla_config& c = a->cfg;
+
+  *p = DecodeProblem{};
+  p->kv = a->kv_cache;
+  p->kv_dtype = a->kv_dtype;
+  p->row_elems = c.kv_lora_rank + c.qk_rope_head_dim;
+  p->total_rows = a->total_rows;
+  p->num_seqs = a->num_seqs;
+  p->seq_len = a->seq_offsets ? 0 : a->seq_len;
+  p->offsets = a->seq_offsets;
+  p->qps = a->queries_per_seq;
+  p->nh = c.num_heads;
+  p->Hq = a->queries_per_seq * c.num_heads;
+  p->q_abs = a->q_absorbed;
+  p->q_rope = a->q_rope;
+  p->W_UV = a->W_UV;
+  p->wuv_dtype = a->w_uv_dtype;
+  p->rope_cos = a->rope_cos;
+  p->rope_sin = a->rope_sin;
+  p->rope_rows = a->rope_rows;
+  p->out = a->output;
+  p->dc = c.kv_lora_rank;
+  p->dR = c.qk_rope_head_dim;
+  p->dv = c.v_head_dim;
+  p->scale_log2 = (float)(kLog2e / std::sqrt((double)(c.qk_nope_head_dim + c.qk_rope_head_dim)));
+
+  if (a->num_seqs == 0) {
+    *plan = Plan{};
+    return LA_SUCCESS;
+  }
+  if (!a->q_rope || !a->W_UV || !a->rope_cos || !a->rope_sin || !a->output) return LA_ERROR_INVALID_VALUE;
+  if (a->total_rows > 0 && !a->kv_cache) return LA_ERROR_INVALID_VALUE;
+
+  Plan pl;
+  const bool mfma_ok = mfma_supported(*p);
+  if (variant == kMfma && !mfma_ok) return LA_ERROR_NOT_SUPPORTED;
+  if (variant == kGeneric || !mfma_ok) {
+    if (!generic_supported(*p)) return LA_ERROR_NOT_SUPPORTED;
+    pl.mfma = false;
+  } else {
+    pl.mfma = true;
+  }
+
+  const int64_t total = a->seq_offsets ? a->total_rows : (int64_t)a->num_seqs * a->seq_len;
+  const int ncu = cu_count();
+  int64_t L;
+  if (chunk_rows > 0) {
+    L = chunk_rows;
+  } else {
+    int64_t groups = pl.mfma ? (p->Hq + mfma_heads_per_group() - 1) / mfma_heads_per_group() : p->Hq;
+    int64_t target_blocks = pl.mfma ? ncu : 4LL * ncu;
+    int64_t chunks = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, groups));
+    L = (total + chunks - 1) / chunks;
+    L = (L + 63) / 64 * 64;
+    L = std::max<int64_t>(L, 64);
+  }
+  if (L > (int64_t)1 << 30) L = (int64_t)1 << 30;
+  if (pl.mfma && L > mfma_max_chunk_rows()) L = mfma_max_chunk_rows();
+  const int64_t nchunks = total > 0 ? (total + L - 1) / L : 0;
+  if (nchunks > (int64_t)1 << 30) return LA_ERROR_INVALID_VALUE;
+  pl.chunk_len = (int)L;
+  pl.num_chunks = (int)nchunks;
+  pl.num_slots = nchunks > 0 ? (int)(nchunks + a->num_seqs - 1) : 0;
+
+  const int64_t tokens = (int64_t)a->num_seqs * a->queries_per_seq;
+  size_t off = 0;
+  if (absorb) {
+    pl.q_abs_off = off;
+    off += align_up((size_t)tokens * c.num_heads * c.kv_lora_rank * sizeof(float));
+  }
+  pl.part_o_off = off;
+  off += align_up((size_t)pl.num_slots * p->Hq * c.kv_lora_rank * sizeof(float));
+  pl.part_lse_off = off;
+  off += align_up((size_t)pl.num_slots * p->Hq * sizeof(float));
+  pl.total = off;
+
+  p->chunk_len = pl.chunk_len;
+  p->num_chunks = pl.num_chunks;
+  p->num_slots = pl.num_slots;
+  *plan = pl;
+  return LA_SUCCESS;
+}
+
+int run(const la_decode_args* a, hipStream_t stream) {
+  DecodeProblem p;
+  Plan plan;
+  int st = prepare(a, &p, &plan);
+  if (st != LA_SUCCESS) return st;
+  if (a->num_seqs == 0) return LA_SUCCESS;
+
+  char* ws = static_cast<char*>(a->workspace);
+  bool owned = false;
+  if (plan.total > 0) {
+    if (ws) {
+      if (a->workspace_bytes < plan.total) return LA_ERROR_WORKSPACE;
+    } else {
+      void* m = nullptr;
+      hipError_t e = hipMallocAsync(&m, plan.total, stream);
+      if (e != hipSuccess) return record_hip(e);
+      ws = static_cast<char*>(m);
+      owned = true;
+    }
+  }
+  auto finish = [&](hipError_t e) -> int {
+    if (owned) {
+      hipError_t f = hipFreeAsync(ws, stream);
+      if (e == hipSuccess) e = f;
+    }
+    return e == hipSuccess ? (int)LA_SUCCESS : record_hip(e);
+  };
+
+  const la_mla_config& c = a->cfg;
+  const int64_t tokens = (int64_t)a->num_seqs * a->queries_per_seq;
+  if (a->q_nope) {
+    float* qa = reinterpret_cast<float*>(ws + plan.q_abs_off);
+    hipError_t e = launch_absorb(a->q_nope, a->W_UK, a->w_uk_dtype, qa, (int)tokens, c.num_heads, c.qk_nope_head_dim,
+                                 c.kv_lora_rank, stream);
+    if (e != hipSuccess) return finish(e);
+    p.q_abs = qa;
+  }
+  p.part_o = reinterpret_cast<float*>(ws + plan.part_o_off);
+  p.part_lse = reinterpret_cast<float*>(ws + plan.part_lse_off);
+  if (plan.num_chunks > 0) {
+    if (a->decode_event_begin) {
+      hipError_t e = hipEventRecord(static_cast<hipEvent_t>(a->decode_event_begin), stream);
+      if (e != hipSuccess) return finish(e);
+    }
+    hipError_t e = plan.mfma ? launch_decode_mfma(p, stream) : launch_decode_generic(p, stream);
+    if (e != hipSuccess) return finish(e);
+    if (a->decode_event_end) {
+      e = hipEventRecord(static_cast<hipEvent_t>(a->decode_event_end), stream);
+      if (e != hipSuccess) return finish(e);
+    }
+  }
+  return finish(launch_combine_project(p, stream));
+}
+
+la_decode_args shared_cache_args(const void* kv_cache, int kv_dtype, int seq_len, int batch, const float* q_absorbed,
+                                 const float* q_rope, const void* W_UV, int w_uv_dtype, const float* rope_cos,
+                                 const float* rope_sin, float* output, const la_mla_config* cfg, void* workspace,
+                                 size_t workspace_bytes) {
+  la_decode_args a{};
+  a.rope_rows = seq_len;
+  a.kv_cache = kv_cache;
+  a.kv_dtype = kv_dtype;
+  a.total_rows = seq_len;
+  a.num_seqs = 1;
+  a.seq_len = seq_len;
+  a.seq_offsets = nullptr;
+  a.queries_per_seq = batch;
+  a.q_absorbed = q_absorbed;
+  a.q_rope = q_rope;
+  a.W_UV = W_UV;
+  a.w_uv_dtype = w_uv_dtype;
+  a.rope_cos = rope_cos;
+  a.rope_sin = rope_sin;
+  a.output = output;
+  if (cfg) a.cfg = *cfg;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  return a;
+}
+
+}  // namespace
+}  // namespace la
+
+extern "C" {
+
+const char* la_status_string(int status) {
+  switch (status) {
+    case LA_SUCCESS: return "success";
+    case LA_ERROR_INVALID_VALUE: return "invalid value";
+    case LA_ERROR_NOT_SUPPORTED: return "not supported";
+    case LA_ERROR_WORKSPACE: return "workspace too small";
+    case LA_ERROR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+int la_last_hip_error(void) { return la::g_last_hip_error; }
+
+int la_abi_version(void) { return LA_ABI_VERSION; }
+
+size_t la_mla_decode_workspace_size(const la_decode_args* args) {
+  la::DecodeProblem p;
+  la::Plan plan;
+  if (la::prepare(args, &p, &plan) != LA_SUCCESS) return 0;
+  return plan.total;
+}
+
+int la_mla_decode(const la_decode_args* args, void* stream) { return la::run(args, static_cast<hipStream_t>(stream)); }
+
+int la_fused_mla(const void* kv_cache, int kv_dtype, int seq_len, const float* q_absorbed, const float* q_rope,
+                 const void* W_UV, int w_uv_dtype, const float* rope_cos, const float* rope_sin, float* output,
+                 const la_mla_config* cfg, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!cfg || seq_len < 0 || !q_absorbed) return LA_ERROR_INVALID_VALUE;
+  la_decode_args a = la::shared_cache_args(kv_cache, kv_dtype, seq_len, 1, q_absorbed, q_rope, W_UV, w_uv_dtype,
+                                           rope_cos, rope_sin, output, cfg, workspace, workspace_bytes);
+  return la::run(&a, static_cast<hipStream_t>(stream));
+}
+
+int la_batched_fused_mla(const void* kv_cache, int kv_dtype, int seq_len, int batch_size, const float* q_absorbed,
+                         const float* q_rope, const void* W_UV, int w_uv_dtype, const float* rope_cos,
+                         const float* rope_sin, float* output, const la_mla_config* cfg, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  if (!cfg || seq_len < 0 || batch_size <= 0 || !q_absorbed) return LA_ERROR_INVALID_VALUE;
+  la_decode_args a = la::shared_cache_args(kv_cache, kv_dtype, seq_len, batch_size, q_absorbed, q_rope, W_UV,
+                                           w_uv_dtype, rope_cos, rope_sin, output, cfg, workspace, workspace_bytes);
+  return la::run(&a, static_cast<hipStream_t>(stream));
+}
+
+size_t la_fused_mla_workspace_size(int seq_len, int batch_size, const la_mla_config* cfg) {
+  if (!cfg || seq_len < 0 || batch_size <= 0) return 0;
+  // Only the plan-relevant fields are read; pointers stay NULL except the ones
+  // the validity checks require to be set.
+  static const float dummy = 0.f;
+  la_decode_args a = la::shared_cache_args(&dummy, LA_DTYPE_F16, seq_len, batch_size, &dummy, &dummy, &dummy,
+                                           LA_DTYPE_F16, &dummy, &dummy, const_cast<float*>(&dummy), cfg, nullptr, 0);
+  la::DecodeProblem p;
+  la::Plan plan;
+  if (la::prepare(&a, &p, &plan) != LA_SUCCESS) return 0;
+  return plan.total;
+}
+
+int la_absorb_q(const float* q_nope, const void* W_UK, int w_uk_dtype, float* q_absorbed, int tokens,
+                const la_mla_config* cfg, void* stream) {
+  if (!la::valid_cfg(cfg) || tokens < 0 || !la::valid_dtype(w_uk_dtype)) return LA_ERROR_INVALID_VALUE;
+  if (tokens == 0) return LA_SUCCESS;
+  if (!q_nope || !W_UK || !q_absorbed) return LA_ERROR_INVALID_VALUE;
+  hipError_t e = la::launch_absorb(q_nope, W_UK, w_uk_dtype, q_absorbed, tokens, cfg->num_heads, cfg->qk_nope_head_dim,
+                                   cfg->kv_lora_rank, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? (int)LA_SUCCESS : la::record_hip(e);
+}
+
+}  // extern "C"

@@ -1,0 +1,133 @@
+// Internal types shared by the HIP kernels and the C-ABI layer of
+// liblatent_attn_hip.so. Not installed; the public ABI is include/latent_attn.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <cstdint>
+
+#include "latent_attn.h"
+
+namespace la {
+
+// log2(e): scores are kept in base-2 units so the softmax uses v_exp_f32 (2^x).
+constexpr float kLog2e = 1.4426950408889634f;
+
+// One decode step, fully resolved on the host. Passed to kernels by value.
+//
+// Sequences: sequence s owns rows [seq_begin(s), seq_begin(s+1)) of the packed
+// cache; RoPE positions are row - seq_begin(s). Each sequence carries Hq query
+// heads = queries_per_seq * nh; query row (s, hq) reads q_abs[(s*Hq + hq)*dc].
+//
+// Split-KV plan: the flat row space is cut into num_chunks chunks of
+// chunk_len rows. The piece of chunk c that falls in sequence s is one
+// "segment"; it writes partial slot (c + s): part_o[(slot*Hq + hq)*dc + i]
+// (normalised by its own softmax sum) and part_lse[slot*Hq + hq] (base-2
+// log-sum-exp of the scaled scores). Slots are unique because a sequence's
+// chunks form a contiguous range that starts no earlier than where the
+// previous sequence's range ends; num_slots = num_chunks + num_seqs - 1.
+struct DecodeProblem {
+  const void* kv;
+  int kv_dtype;
+  int row_elems;  // dc + dR
+  int64_t total_rows;
+  int num_seqs;
+  int seq_len;            // used when offsets == nullptr
+  const int32_t* offsets; // device, num_seqs + 1, or nullptr
+  int qps;                // query tokens per sequence
+  int nh;                 // weight heads
+  int Hq;                 // query heads per sequence = qps * nh
+  const float* q_abs;     // (num_seqs*Hq, dc) f32
+  const float* q_rope;    // (num_seqs*Hq, dR) f32
+  const void* W_UV;
+  int wuv_dtype;
+  const float* rope_cos;
+  const float* rope_sin;
+  int64_t rope_rows;      // 0 = unchecked
+  float* out;             // (num_seqs*Hq, dv)
+  int dc, dR, dv;
+  float scale_log2;       // softmax scale * log2(e)
+  // plan
+  int chunk_len;
+  int num_chunks;
+  int num_slots;
+  float* part_o;
+  float* part_lse;
+};
+
+// First row of sequence s, clamped into [0, total_rows] so that malformed
+// offsets can give wrong answers but never out-of-bounds reads.
+__device__ inline int64_t seq_begin(const DecodeProblem& p, int s) {
+  const int64_t b = p.offsets ? (int64_t)p.offsets[s] : (int64_t)s * p.seq_len;
+  return b < 0 ? 0 : (b > p.total_rows ? p.total_rows : b);
+}
+
+// RoPE table row of in-sequence position pos.
+__device__ inline int64_t rope_row(const DecodeProblem& p, int64_t pos) {
+  return (p.rope_rows > 0 && pos >= p.rope_rows) ? p.rope_rows - 1 : pos;
+}
+
+// Sequence whose row range contains row r: the largest s with
+// seq_begin(s) <= r (empty sequences are skipped because their successor has
+// the same begin). Requires seq_begin(0) <= r < seq_begin(num_seqs).
+__device__ inline int find_seq(const DecodeProblem& p, int64_t r) {
+  if (!p.offsets) return (int)(r / p.seq_len);
+  int lo = 0, hi = p.num_seqs - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if ((int64_t)p.offsets[mid] <= r) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+template <typename T>
+__device__ inline float to_f32(T v);
+template <>
+__device__ inline float to_f32<float>(float v) { return v; }
+template <>
+__device__ inline float to_f32<__half>(__half v) { return __half2float(v); }
+template <>
+__device__ inline float to_f32<__hip_bfloat16>(__hip_bfloat16 v) { return __bfloat162float(v); }
+
+// Load element i of a weight matrix whose dtype is only known at run time
+// (uniform across the launch, so the switch does not diverge).
+__device__ inline float load_any(const void* base, int dtype, int64_t i) {
+  if (dtype == LA_DTYPE_BF16) return __bfloat162float(reinterpret_cast<const __hip_bfloat16*>(base)[i]);
+  if (dtype == LA_DTYPE_F16) return __half2float(reinterpret_cast<const __half*>(base)[i]);
+  return reinterpret_cast<const float*>(base)[i];
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// ---- host launchers (one per kernel family) -------------------------------
+
+// VALU split-KV decode: any dtype, kv_lora_rank <= 1024, qk_rope_head_dim <= 256.
+hipError_t launch_decode_generic(const DecodeProblem& p, hipStream_t stream);
+bool generic_supported(const DecodeProblem& p);
+
+// MFMA split-KV decode for 16-bit caches with kv_lora_rank 512, qk_rope_head_dim 64.
+hipError_t launch_decode_mfma(const DecodeProblem& p, hipStream_t stream);
+bool mfma_supported(const DecodeProblem& p);
+int mfma_heads_per_group();
+int mfma_max_chunk_rows();
+
+// log-sum-exp combine of the partial slots + W_UV projection into p.out.
+hipError_t launch_combine_project(const DecodeProblem& p, hipStream_t stream);
+
+// q_abs = q_nope . W_UK per head.
+hipError_t launch_absorb(const float* q_nope, const void* W_UK, int w_dtype, float* q_abs, int tokens, int nh, int dn,
+                         int dc, hipStream_t stream);
+
+}  // namespace la

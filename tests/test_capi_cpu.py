@@ -1,0 +1,151 @@
+"""CPU checks of the C ABI and the torch extension's argument validation.
+
+No kernels run here: only symbol export, ABI constants, argument rejection
+(which happens before any HIP call) and the extension's input checks, which
+mirror the reference's TORCH_CHECKs (reference csrc/bindings.cpp:28-40,
+147-152, 208-221).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+from latent_attn import MLAConfig, capi
+from latent_attn import functional as F
+
+
+def test_library_exports_header_symbols():
+    lib = capi.load()
+    names = capi.header_symbols()
+    assert {"la_mla_decode", "la_fused_mla", "la_batched_fused_mla", "la_absorb_q"} <= set(names)
+    for n in names:
+        assert hasattr(lib, n), n
+    assert lib.la_abi_version() == 1
+
+
+def test_status_strings():
+    lib = capi.load()
+    assert lib.la_status_string(capi.LA_SUCCESS) == b"success"
+    assert lib.la_status_string(capi.LA_ERROR_INVALID_VALUE) == b"invalid value"
+    assert lib.la_status_string(capi.LA_ERROR_WORKSPACE) == b"workspace too small"
+    assert lib.la_status_string(99) == b"unknown status"
+
+
+def _args(**kw):
+    a = capi.DecodeArgs()
+    a.cfg = capi.config(MLAConfig.deepseek_v2())
+    a.kv_dtype = capi.LA_DTYPE_BF16
+    a.w_uv_dtype = capi.LA_DTYPE_BF16
+    a.w_uk_dtype = capi.LA_DTYPE_BF16
+    a.num_seqs = 1
+    a.queries_per_seq = 1
+    a.seq_len = 16
+    a.total_rows = 16
+    fake = 0x1000
+    a.kv_cache = a.q_rope = a.W_UV = a.rope_cos = a.rope_sin = a.output = a.q_absorbed = fake
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("field,value", [
+    ("queries_per_seq", 0),
+    ("num_seqs", -1),
+    ("seq_len", -3),
+    ("total_rows", 8),          # uniform sequences need num_seqs*seq_len rows
+    ("kv_dtype", 7),
+    ("q_absorbed", 0),          # neither q_nope nor q_absorbed
+    ("q_nope", 0x2000),         # both q_nope and q_absorbed
+    ("chunk_rows", -1),
+    ("kernel_variant", 5),
+    ("q_rope", 0),
+    ("output", 0),
+])
+def test_decode_rejects_bad_arguments(field, value):
+    lib = capi.load()
+    a = _args(**{field: value})
+    assert lib.la_mla_decode(ctypes.byref(a), None) == capi.LA_ERROR_INVALID_VALUE
+
+
+def test_decode_rejects_bad_config():
+    lib = capi.load()
+    a = _args()
+    a.cfg.qk_rope_head_dim = 63  # odd: rotate-half needs pairs
+    assert lib.la_mla_decode(ctypes.byref(a), None) == capi.LA_ERROR_INVALID_VALUE
+    a = _args()
+    a.cfg.num_heads = 0
+    assert lib.la_mla_decode(ctypes.byref(a), None) == capi.LA_ERROR_INVALID_VALUE
+    assert lib.la_mla_decode(None, None) == capi.LA_ERROR_INVALID_VALUE
+
+
+def test_empty_batch_is_a_no_op():
+    lib = capi.load()
+    a = _args(num_seqs=0, total_rows=0)
+    assert lib.la_mla_decode(ctypes.byref(a), None) == capi.LA_SUCCESS
+
+
+def test_absorb_rejects_bad_arguments():
+    lib = capi.load()
+    cfg = capi.config(MLAConfig.deepseek_v2())
+    assert lib.la_absorb_q(None, None, 2, None, -1, ctypes.byref(cfg), None) == capi.LA_ERROR_INVALID_VALUE
+    assert lib.la_absorb_q(None, None, 2, None, 0, ctypes.byref(cfg), None) == capi.LA_SUCCESS
+    assert lib.la_absorb_q(0x10, 0x10, 9, 0x10, 1, ctypes.byref(cfg), None) == capi.LA_ERROR_INVALID_VALUE
+
+
+# ---- torch extension checks (CPU tensors never reach the library) ----------
+
+def _fused_inputs(dtype=torch.float16, S=8, nh=4):
+    cfg = MLAConfig(5120, 512, 128, 64, nh, 128)
+    kv = torch.zeros(S, 576, dtype=dtype)
+    qa = torch.zeros(nh, 512)
+    qr = torch.zeros(nh, 64)
+    W = torch.zeros(nh * 128, 512, dtype=dtype)
+    c = torch.zeros(S, 32)
+    return cfg, kv, qa, qr, W, c
+
+
+def test_extension_requires_device_tensors():
+    cfg, kv, qa, qr, W, c = _fused_inputs()
+    with pytest.raises(RuntimeError, match="kv_cache must be on CUDA"):
+        F.fused_mla(kv, qa, qr, W, c, c, cfg)
+
+
+def test_extension_dtype_and_layout_messages():
+    cfg, kv, qa, qr, W, c = _fused_inputs()
+    with pytest.raises(RuntimeError, match="kv_cache must be float16, bfloat16 or float32"):
+        F.fused_mla(kv.to(torch.int32), qa, qr, W, c, c, cfg)
+    with pytest.raises(RuntimeError, match="kv_cache must be contiguous"):
+        F.fused_mla(kv.t(), qa, qr, W, c, c, cfg)
+
+
+def test_config_validation_messages():
+    """MLAConfig.validate raises like src/mla_config.cuh:35-40 (the extension
+    raises the same ValueError after its tensor checks; see the GPU tests)."""
+    with pytest.raises(ValueError, match="MLA dims must be positive"):
+        MLAConfig(5120, 0, 128, 64, 4, 128).validate()
+    with pytest.raises(ValueError, match="num_heads and v_head_dim must be positive"):
+        MLAConfig(5120, 512, 128, 64, 0, 128).validate()
+    MLAConfig.deepseek_v2().validate()
+
+
+def test_batched_rejects_2d_queries():
+    cfg, kv, qa, qr, W, c = _fused_inputs()
+    with pytest.raises(RuntimeError):
+        F.batched_fused_mla(kv, qa, qr, W, c, c, cfg)
+
+
+def test_functional_signatures_match_reference():
+    import inspect
+
+    assert list(inspect.signature(F.fused_mla).parameters) == [
+        "kv_cache", "q_absorbed", "q_rope", "W_UV", "rope_cos", "rope_sin", "cfg"]
+    assert list(inspect.signature(F.naive_mla).parameters) == [
+        "kv_cache", "W_UK", "W_UV", "q_nope", "q_rope", "rope_cos", "rope_sin", "cfg"]
+    assert list(inspect.signature(F.batched_fused_mla).parameters) == [
+        "kv_cache", "q_absorbed", "q_rope", "W_UV", "rope_cos", "rope_sin", "cfg"]
+    assert MLAConfig.deepseek_v2() == MLAConfig(5120, 512, 128, 64, 128, 128)
+    assert MLAConfig.deepseek_v3() == MLAConfig(7168, 512, 128, 64, 128, 128)
+    assert MLAConfig.deepseek_v2().bytes_per_kv_entry() == 1152
