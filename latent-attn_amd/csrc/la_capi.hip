@@ -187,8 +187,13 @@ int run(const la_decode_args* a, hipStream_t stream) {
   const int64_t tokens = (int64_t)a->num_seqs * a->queries_per_seq;
   if (a->q_nope) {
     float* qa = reinterpret_cast<float*>(ws + plan.q_abs_off);
-    hipError_t e = launch_absorb(a->q_nope, a->W_UK, a->w_uk_dtype, qa, (int)tokens, c.num_heads, c.qk_nope_head_dim,
-                                 c.kv_lora_rank, stream);
+    hipError_t e =
+        absorb_mfma_supported(a->w_uk_dtype, c.num_heads, c.qk_nope_head_dim, c.kv_lora_rank) &&
+                (reinterpret_cast<uintptr_t>(a->q_nope) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->W_UK) & 15) == 0
+            ? launch_absorb_mfma(a->q_nope, a->W_UK, a->w_uk_dtype, qa, (int)tokens, c.num_heads,
+                                 c.qk_nope_head_dim, c.kv_lora_rank, stream)
+            : launch_absorb(a->q_nope, a->W_UK, a->w_uk_dtype, qa, (int)tokens, c.num_heads, c.qk_nope_head_dim,
+                            c.kv_lora_rank, stream);
     if (e != hipSuccess) return finish(e);
     p.q_abs = qa;
   }
@@ -206,7 +211,8 @@ int run(const la_decode_args* a, hipStream_t stream) {
       if (e != hipSuccess) return finish(e);
     }
   }
-  return finish(launch_combine_project(p, stream));
+  return finish(project_mfma_supported(p) ? launch_combine_project_mfma(p, stream)
+                                           : launch_combine_project(p, stream));
 }
 
 la_decode_args shared_cache_args(const void* kv_cache, int kv_dtype, int seq_len, int batch, const float* q_absorbed,
@@ -285,15 +291,23 @@ int la_batched_fused_mla(const void* kv_cache, int kv_dtype, int seq_len, int ba
 
 size_t la_fused_mla_workspace_size(int seq_len, int batch_size, const la_mla_config* cfg) {
   if (!cfg || seq_len < 0 || batch_size <= 0) return 0;
-  // Only the plan-relevant fields are read; pointers stay NULL except the ones
-  // the validity checks require to be set.
-  static const float dummy = 0.f;
-  la_decode_args a = la::shared_cache_args(&dummy, LA_DTYPE_F16, seq_len, batch_size, &dummy, &dummy, &dummy,
-                                           LA_DTYPE_F16, &dummy, &dummy, const_cast<float*>(&dummy), cfg, nullptr, 0);
-  la::DecodeProblem p;
-  la::Plan plan;
-  if (la::prepare(&a, &p, &plan) != LA_SUCCESS) return 0;
-  return plan.total;
+  // Only plan-relevant fields are read. The kernel family is not known here
+  // (it depends on dtype and pointer alignment), so return the larger of the
+  // two plans.
+  alignas(256) static const char dummy[256] = {0};
+  const float* d = reinterpret_cast<const float*>(dummy);
+  size_t best = 0;
+  for (int variant : {1, 2}) {
+    for (int dt : {LA_DTYPE_F16, LA_DTYPE_F32}) {
+      la_decode_args a = la::shared_cache_args(dummy, dt, seq_len, batch_size, d, d, dummy, dt, d, d,
+                                               const_cast<float*>(d), cfg, nullptr, 0);
+      a.kernel_variant = variant;
+      la::DecodeProblem p;
+      la::Plan plan;
+      if (la::prepare(&a, &p, &plan) == LA_SUCCESS && plan.total > best) best = plan.total;
+    }
+  }
+  return best;
 }
 
 int la_absorb_q(const float* q_nope, const void* W_UK, int w_uk_dtype, float* q_absorbed, int tokens,
@@ -301,8 +315,12 @@ int la_absorb_q(const float* q_nope, const void* W_UK, int w_uk_dtype, float* q_
   if (!la::valid_cfg(cfg) || tokens < 0 || !la::valid_dtype(w_uk_dtype)) return LA_ERROR_INVALID_VALUE;
   if (tokens == 0) return LA_SUCCESS;
   if (!q_nope || !W_UK || !q_absorbed) return LA_ERROR_INVALID_VALUE;
-  hipError_t e = la::launch_absorb(q_nope, W_UK, w_uk_dtype, q_absorbed, tokens, cfg->num_heads, cfg->qk_nope_head_dim,
-                                   cfg->kv_lora_rank, static_cast<hipStream_t>(stream));
+  const bool mfma = la::absorb_mfma_supported(w_uk_dtype, cfg->num_heads, cfg->qk_nope_head_dim, cfg->kv_lora_rank) &&
+                    (reinterpret_cast<uintptr_t>(q_nope) & 15) == 0 && (reinterpret_cast<uintptr_t>(W_UK) & 15) == 0;
+  hipError_t e = mfma ? la::launch_absorb_mfma(q_nope, W_UK, w_uk_dtype, q_absorbed, tokens, cfg->num_heads,
+                                               cfg->qk_nope_head_dim, cfg->kv_lora_rank, static_cast<hipStream_t>(stream))
+                      : la::launch_absorb(q_nope, W_UK, w_uk_dtype, q_absorbed, tokens, cfg->num_heads,
+                                          cfg->qk_nope_head_dim, cfg->kv_lora_rank, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? (int)LA_SUCCESS : la::record_hip(e);
 }
 

@@ -126,6 +126,13 @@ int mfma_max_chunk_rows();
 // log-sum-exp combine of the partial slots + W_UV projection into p.out.
 hipError_t launch_combine_project(const DecodeProblem& p, hipStream_t stream);
 
+// MFMA versions for 16-bit weights (la_proj.hip).
+bool absorb_mfma_supported(int w_dtype, int nh, int dn, int dc);
+hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype, float* q_abs, int tokens, int nh,
+                              int dn, int dc, hipStream_t stream);
+bool project_mfma_supported(const DecodeProblem& p);
+hipError_t launch_combine_project_mfma(const DecodeProblem& p, hipStream_t stream);
+
 // q_abs = q_nope . W_UK per head.
 hipError_t launch_absorb(const float* q_nope, const void* W_UK, int w_dtype, float* q_abs, int tokens, int nh, int dn,
                          int dc, hipStream_t stream);

@@ -8,30 +8,35 @@
 //   RoPE rotate-half, pairs (i, i+32), cos/sin rows by position  src/fused_mla.cu:34-54
 //   acc[h] = sum_pos softmax_pos(s[h,:]) * c_t[pos]    src/fused_mla.cu:240-256
 // The reference computes this on one thread per head; here one workgroup
-// streams a chunk of the cache for a group of up to 64 heads.
+// streams a chunk of the cache once for a group of up to 128 heads.
 //
-// Work decomposition. 1-D grid over (chunk, head group); the head groups of one
-// chunk get block ids 8 apart, so they run on the same XCD at about the same
-// time and the second read of every tile is an L2 hit. 512 threads = 8 waves.
-// A block walks the segments of its chunk (pieces of the chunk inside one
+// Work decomposition. 1-D grid over (chunk, head group); when there are
+// several head groups, the groups of one chunk get block ids 8 apart (same
+// XCD under round-robin dispatch, so re-reads of a tile hit L2). 256 threads
+// = 4 waves, one per SIMD; wave w owns heads [32w, 32w+32) of the group. A
+// block walks the segments of its chunk (pieces of the chunk inside one
 // sequence) in tiles of 32 positions:
-//   * Staging: each tile (32 rows x 1152 B, one contiguous HBM range) and its
-//     cos/sin rows are copied HBM->LDS with global_load_lds_dwordx4 (no VGPR
-//     staging), up to three tiles in flight. Inside a row the 16-B chunk j
-//     lives at chunk j ^ (row & 7), so 16 lanes reading 16 rows at one column
-//     hit distinct banks. k_rope is rotated in place in LDS once per position
-//     (shared by all heads).
-//   * Scores: wave w computes S[16 heads x 16 positions] for head block w&3
-//     and position half w>>2 with v_mfma_f32_16x16x32 (A = Q in VGPRs as
-//     16-bit, pre-scaled by scale*log2(e); B = 16-B reads of tile rows).
-//   * Online softmax in base 2 (running max m shared by the two position
-//     halves through LDS, per-half running sums l); P (16-bit) and the rescale
-//     factor alpha go to LDS.
-//   * PV: wave w owns latent columns [64w, 64w+64) of O for all 64 heads:
-//     O += P[64 x 32] . Tile[32 x 64] with v_mfma_f32_32x32x16 (A = P rows,
-//     B = tile columns via ds_read_b64_tr_b16).
-//   * At a segment end O / l and the base-2 log-sum-exp m + log2(l) go to the
-//     partial slot (chunk + sequence); a later kernel merges the slots.
+//   * Staging: per tile, wave w copies rows 8w..8w+7 HBM->LDS with
+//     global_load_lds_dwordx4 (c_t rows, k_rope rows, cos and sin rows: 11
+//     copies per wave, no VGPR staging) into a 3-deep ring, two tiles ahead.
+//     Inside a row the 16-B chunk j lives at chunk j ^ f(row),
+//     f(row) = 2(row&3) | ((row>>2)&1): 8 consecutive rows at one column and
+//     4 consecutive rows at two adjacent columns both land in distinct banks.
+//     Each wave rotates (RoPE) the k_rope rows it copied itself, so only its
+//     own vmcnt has to drain; one s_barrier per tile publishes the tile.
+//   * Scores: S^T[32 pos x 32 heads] = sum over 36 k-steps of
+//     v_mfma_f32_32x32x16(A = 16 B of a tile row, B = Q^T). Q (pre-scaled by
+//     scale*log2(e), 16-bit) stays in 144 VGPRs.
+//   * Softmax in base 2, lazily rescaled: P = 2^(s - m) with a running max m
+//     that is only raised when a score exceeds it by more than 8 (then O and
+//     the running sum are rescaled). P <= 2^8 is exact enough in 16 bits and
+//     the 256 O accumulators are almost never touched outside the MFMAs.
+//   * PV: O[32 heads x 512] += P[32 x 32] . Tile[32 x 512]: the S^T
+//     accumulator layout already is the A-operand layout of P (lane = head,
+//     8 positions per k-step), so P never goes through LDS; B = tile columns
+//     via ds_read_b64_tr_b16.
+//   * At a segment end O / l and the base-2 log-sum-exp m + log2(l) go to
+//     partial slot (chunk + sequence); la_proj.hip merges the slots.
 #include "la_internal.hpp"
 
 #include <cstring>
@@ -42,25 +47,21 @@ namespace {
 
 constexpr int kDc = 512;
 constexpr int kDr = 64;
-constexpr int kRow = kDc + kDr;       // elements per cache row
-constexpr int kRowBytes = kRow * 2;   // 1152
-constexpr int kT = 32;                // positions per tile
-constexpr int kWaves = 8;
+constexpr int kT = 32;                 // positions per tile
+constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kHG = 64;               // heads per group (block)
-constexpr int kNHB = kHG / 32;        // 32-head blocks in PV
-constexpr int kTileBytes = kT * kRowBytes;      // 36864
-constexpr int kTabBytes = kT * (kDr / 2) * 4;   // 4096: 32 rows of 32 floats
-constexpr int kBufBytes = kTileBytes + 2 * kTabBytes;
+constexpr int kHG = 128;               // heads per group (block)
+constexpr int kCtBytes = kT * kDc * 2;       // 32768: c_t rows, 1024 B each
+constexpr int kRopeOff = kCtBytes;           // k_rope rows, 128 B each
+constexpr int kCosOff = kRopeOff + kT * 128; // cos rows (32 floats)
+constexpr int kSinOff = kCosOff + kT * 128;  // sin rows
+constexpr int kBufBytes = kSinOff + kT * 128;  // 45056
 constexpr int kNBuf = 3;
-constexpr int kPRowBytes = 80;                  // 32 x 16-bit P + 16 B pad
-constexpr int kPOff = kNBuf * kBufBytes;
-constexpr int kAlphaOff = kPOff + kHG * kPRowBytes;
-constexpr int kTmaxOff = kAlphaOff + kHG * 4;   // [2][kHG] tile maxima per position half
-constexpr int kLsumOff = kTmaxOff + 2 * kHG * 4;  // [2][kHG] running sums per half
-constexpr int kInvLOff = kLsumOff + 2 * kHG * 4;
-constexpr int kLdsBytes = kInvLOff + kHG * 4;
-constexpr int kDmaPerTile = kTileBytes / 1024 + 2 * kTabBytes / 1024;  // 44
+constexpr int kScratchOff = kNBuf * kBufBytes;  // per-wave 32 floats
+constexpr int kQropeOff = kScratchOff + kWaves * 32 * 4;  // q_rope of the group: 128 rows x 128 B
+constexpr int kLdsBytes = kQropeOff + kHG * kDr * 2;
+constexpr int kDmaPerWave = 11;        // 8 c_t rows + k_rope + cos + sin
+constexpr int kRescaleSlack = 8;       // log2 units before the running max moves
 // Longest chunk the kernel accepts: keeps row byte offsets inside 32 bits.
 constexpr int kMaxChunkRows = 1 << 20;
 
@@ -75,19 +76,33 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Element-type traits: MFMA operand vector and instructions per 16-bit type.
 template <typename KT>
 struct Ops;
 
+// The attention kernel issues its MFMAs as inline asm so that the register
+// classes are fixed: the score tile S accumulates in VGPRs (mma_v0 / mma_v)
+// and the 256 O accumulators stay in AGPRs (mma_a) across the tile loop --
+// left to itself the compiler puts both in AGPRs and spills. The compiler
+// does not see inside the asm, so wait states are explicit: a VALU read of an
+// MFMA result goes after settle()/settle_acc() (32 wait states), an MFMA that
+// reads VALU-written operands after operands_ready() (8 wait states). Chained
+// MFMAs on the same accumulator need none (the hardware interlocks srcC ==
+// vdst of the same opcode).
 template <>
 struct Ops<__hip_bfloat16> {
   typedef bf16x8 vec;
   typedef __bf16 elem;
-  static __device__ inline f32x4 mma16(vec a, vec b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-  static __device__ inline f32x16 mma32(vec a, vec b, f32x16 c) {
+  static __device__ inline f32x16 mma(vec a, vec b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ inline void mma_v0(f32x16& d, vec a, vec b) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+  }
+  static __device__ inline void mma_v(f32x16& d, vec a, vec b) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+  }
+  static __device__ inline void mma_a(f32x16& d, vec a, vec b) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
   }
 };
 
@@ -95,85 +110,149 @@ template <>
 struct Ops<__half> {
   typedef f16x8 vec;
   typedef _Float16 elem;
-  static __device__ inline f32x4 mma16(vec a, vec b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-  static __device__ inline f32x16 mma32(vec a, vec b, f32x16 c) {
+  static __device__ inline f32x16 mma(vec a, vec b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
+  static __device__ inline void mma_v0(f32x16& d, vec a, vec b) {
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+  }
+  static __device__ inline void mma_v(f32x16& d, vec a, vec b) {
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+  }
+  static __device__ inline void mma_a(f32x16& d, vec a, vec b) {
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
+  }
 };
 
-// Byte offset of logical 16-B chunk j of tile row `row` (XOR swizzle).
-__device__ inline int swz(int row, int j) { return row * kRowBytes + ((j ^ (row & 7)) << 4); }
+// 32 wait states after the last inline-asm MFMA writing d0/d1 and before any
+// other instruction reads them (covers the MFMA-result -> VALU read hazard
+// for up to 16-pass MFMAs). Taking d0/d1 as in-out operands orders every
+// later use after it.
+__device__ inline void settle(f32x16& d0, f32x16& d1) {
+  asm volatile("s_nop 15\n\ts_nop 15" : "+v"(d0), "+v"(d1));
+}
 
-__device__ inline void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+__device__ inline void settle1(f32x16& d0) { asm volatile("s_nop 15\n\ts_nop 15" : "+v"(d0)); }
 
-// LDS-visibility barrier that leaves outstanding HBM->LDS copies in flight:
-// waits for this wave's LDS operations only, then s_barrier. The "memory"
-// clobber keeps the compiler from moving LDS accesses across it.
+// 32 wait states before the O accumulators (AGPRs written by MFMAs) are read
+// or rewritten by VALU code; every later access is ordered after it.
+__device__ inline void settle_acc(f32x16 (&acc)[16]) {
+  asm volatile("s_nop 15\n\ts_nop 15" : "+a"(acc[0]), "+a"(acc[1]), "+a"(acc[2]), "+a"(acc[3]), "+a"(acc[4]),
+               "+a"(acc[5]), "+a"(acc[6]), "+a"(acc[7]), "+a"(acc[8]), "+a"(acc[9]), "+a"(acc[10]), "+a"(acc[11]),
+               "+a"(acc[12]), "+a"(acc[13]), "+a"(acc[14]), "+a"(acc[15]));
+}
+
+// Forces one accumulator block back into AGPRs at this point (no code).
+__device__ inline void pin_agpr(f32x16& d) { asm volatile("" : "+a"(d)); }
+
+// 8 wait states between VALU/v_accvgpr_write producers and MFMA consumers.
+template <typename V>
+__device__ inline void operands_ready(V& a, V& b) {
+  asm volatile("s_nop 7" : "+v"(a), "+v"(b));
+}
+__device__ inline void acc_ready(f32x16 (&acc)[16]) {
+  asm volatile("s_nop 7" : "+a"(acc[0]), "+a"(acc[1]), "+a"(acc[2]), "+a"(acc[3]), "+a"(acc[4]), "+a"(acc[5]),
+               "+a"(acc[6]), "+a"(acc[7]), "+a"(acc[8]), "+a"(acc[9]), "+a"(acc[10]), "+a"(acc[11]), "+a"(acc[12]),
+               "+a"(acc[13]), "+a"(acc[14]), "+a"(acc[15]));
+}
+
+__device__ inline int swzf(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+
+// vmcnt(n) with the other counters left alone (gfx9 encoding, n < 16).
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+// LDS-visibility barrier that leaves outstanding HBM->LDS copies in flight.
+// The "memory" clobber keeps the compiler from moving LDS accesses across it.
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <typename T>
-__device__ inline T lds_load(const char* base, int off) {
-  return *reinterpret_cast<const T*>(base + off);
+// Returns x through an empty asm: values computed from the result cannot be
+// hoisted out of the enclosing loop. Used on the lane index at the top of each
+// tile so per-lane addresses are recomputed (a few VALU ops) instead of being
+// kept live across the loop in dozens of VGPRs.
+__device__ inline int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
 }
 
-struct SegCtx {
-  const char* base;   // first byte of the segment's first row
-  int64_t seg_lo;     // first row of the segment
-  int64_t seg_hi;     // one past the last row
-  int64_t pos0;       // in-sequence position of seg_lo
-  int last;           // index of the segment's last row, relative to seg_lo
+// LDS is addressed with 32-bit byte offsets from the start of the dynamic LDS
+// block (address-space-3 pointers), never with 64-bit generic pointers.
+typedef __attribute__((address_space(3))) char lchar;
+
+template <typename T>
+__device__ inline T lds_ld(const lchar* L, uint32_t off) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) T*>(L + off);
+}
+template <typename T>
+__device__ inline void lds_st(lchar* L, uint32_t off, T v) {
+  *reinterpret_cast<__attribute__((address_space(3))) T*>(L + off) = v;
+}
+// ds_read_b64_tr_b16 as inline asm: the builtin makes the compiler assume the
+// read may alias the in-flight HBM->LDS copies and drain vmcnt before it. The
+// asm result must not be used before b_wait() (lgkmcnt).
+__device__ inline i16x4 lds_tr(const lchar* L, uint32_t off) {
+  i16x4 r;
+  const uint32_t addr = (uint32_t)(uintptr_t)(L + off);
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+
+struct TrPair {
+  i16x4 x0, x1;
 };
 
-// Issue this wave's share of the HBM->LDS copies for tile k of the segment
-// into buffer `buf`. Addresses are a wave-uniform base plus a 32-bit lane
+struct SegCtx {
+  const char* base;  // first byte of the segment's first row
+  int64_t pos0;      // in-sequence position of the segment's first row
+  int last;          // index of the segment's last row, relative to its first
+};
+
+// Wave w's 11 HBM->LDS copies for tile k into the buffer at LDS offset buf:
+// c_t of rows 8w..8w+7 (one copy per row), then their k_rope, cos and sin rows
+// (one copy each). Global addresses are a wave-uniform base plus a 32-bit lane
 // offset (segments are capped at kMaxChunkRows rows, tables at 2^24 rows).
-// Rows past the segment end re-read its last row (their scores are masked);
-// cos/sin rows are clamped the same way and to the table.
-__device__ inline void issue_tile_dma(const DecodeProblem& p, const SegCtx& sg, int k, char* buf, int wave,
-                                      int lane) {
-  const int r0 = k * kT;
-  for (int ii = wave; ii < kDmaPerTile; ii += kWaves) {
-    const char* src;
-    char* dst;
-    if (ii < kTileBytes / 1024) {
-      const int q = ii * 64 + lane;  // physical 16-B chunk index inside the tile
-      const int row = q / 72, jp = q - row * 72;
-      const int j = jp ^ (row & 7);
-      const int r = min(r0 + row, sg.last);
-      src = sg.base + (uint32_t)(r * kRowBytes + j * 16);
-      dst = buf + ii * 1024;
-    } else {
-      const int t = ii - kTileBytes / 1024;  // 0..3 cos, 4..7 sin
-      const int part = t & 3;
-      const int r = min(r0 + part * 8 + (lane >> 3), sg.last);
-      const int pos = (int)rope_row(p, sg.pos0 + r);
-      const char* tab = reinterpret_cast<const char*>(t < 4 ? p.rope_cos : p.rope_sin);
-      src = tab + (uint32_t)(pos * (kDr / 2 * 4) + (lane & 7) * 16);
-      dst = buf + kTileBytes + (t < 4 ? 0 : kTabBytes) + part * 1024;
-    }
-    __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
+// Rows past the segment end re-read its last row; their scores are masked.
+__device__ inline void issue_tile_dma(const DecodeProblem& p, const SegCtx& sg, int k, lchar* L, uint32_t buf,
+                                      int wave, int lane) {
+  const int r_first = 8 * wave;
+#pragma unroll
+  for (int rr = 0; rr < 8; ++rr) {
+    const int row = r_first + rr;
+    const int r = min(k * kT + row, sg.last);
+    const int j = lane ^ swzf(rr);  // row & 7 == rr
+    __builtin_amdgcn_global_load_lds(sg.base + (uint32_t)(r * (kDc + kDr) * 2 + j * 16),
+                                     (lds_void*)(L + buf + row * 1024), 16, 0, 0);
   }
+  const int row = r_first + (lane >> 3);
+  const int r = min(k * kT + row, sg.last);
+  const int jr = (lane & 7) ^ swzf(lane >> 3);  // row & 7 == lane >> 3
+  __builtin_amdgcn_global_load_lds(sg.base + (uint32_t)(r * (kDc + kDr) * 2 + kDc * 2 + jr * 16),
+                                   (lds_void*)(L + buf + kRopeOff + r_first * 128), 16, 0, 0);
+  const uint32_t toff = (uint32_t)(rope_row(p, sg.pos0 + r) * (kDr / 2) * 4 + (lane & 7) * 16);
+  __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(p.rope_cos) + toff,
+                                   (lds_void*)(L + buf + kCosOff + r_first * 128), 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(p.rope_sin) + toff,
+                                   (lds_void*)(L + buf + kSinOff + r_first * 128), 16, 0, 0);
 }
 
-// Rotate-half RoPE of the tile's k_rope in place (src/fused_mla.cu:43-51):
-// r[i] = k[i]*c - k[i+32]*s, r[i+32] = k[i]*s + k[i+32]*c. Threads 0..255,
-// each 4 consecutive i of one row.
+// Rotate-half RoPE of rows 8w..8w+7 of the tile at LDS offset buf, in place
+// (src/fused_mla.cu:43-51): r[i] = k[i]*c - k[i+32]*s, r[i+32] = k[i]*s +
+// k[i+32]*c. Lane: row 8w + lane/8, pairs i = 4(lane%8) .. +3.
 template <typename KT>
-__device__ inline void rotate_tile(char* buf, int tid) {
+__device__ inline void rotate_rows(lchar* L, uint32_t buf, int wave, int lane) {
   typedef typename Ops<KT>::elem E;
-  if (tid >= kT * 8) return;
-  const int row = tid >> 3, u = tid & 7;
-  const int i0 = u * 4;                        // 0..28
-  const int ja = 64 + (i0 >> 3), jb = ja + 4;  // chunks holding k[i0], k[i0+32]
-  const int sub = (i0 & 7) * 2;                // byte offset inside the chunk
-  char* pa = buf + swz(row, ja) + sub;
-  char* pb = buf + swz(row, jb) + sub;
-  const i16x4 ka = *reinterpret_cast<i16x4*>(pa);
-  const i16x4 kb = *reinterpret_cast<i16x4*>(pb);
-  const f32x4 c = *reinterpret_cast<const f32x4*>(buf + kTileBytes + row * 128 + i0 * 4);
-  const f32x4 s = *reinterpret_cast<const f32x4*>(buf + kTileBytes + kTabBytes + row * 128 + i0 * 4);
+  const int rl = lane >> 3, u = lane & 7;
+  const int row = 8 * wave + rl;
+  const int f = swzf(rl);
+  const uint32_t pa = buf + kRopeOff + row * 128 + (((u >> 1) ^ f) << 4) + 8 * (u & 1);
+  const uint32_t pb = buf + kRopeOff + row * 128 + (((4 + (u >> 1)) ^ f) << 4) + 8 * (u & 1);
+  const i16x4 ka = lds_ld<i16x4>(L, pa);
+  const i16x4 kb = lds_ld<i16x4>(L, pb);
+  const f32x4 c = lds_ld<f32x4>(L, buf + kCosOff + row * 128 + 16 * u);
+  const f32x4 s = lds_ld<f32x4>(L, buf + kSinOff + row * 128 + 16 * u);
   i16x4 ra, rb;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -182,14 +261,18 @@ __device__ inline void rotate_tile(char* buf, int tid) {
     ra[e] = __builtin_bit_cast(short, (E)(k0 * c[e] - k1 * s[e]));
     rb[e] = __builtin_bit_cast(short, (E)(k0 * s[e] + k1 * c[e]));
   }
-  *reinterpret_cast<i16x4*>(pa) = ra;
-  *reinterpret_cast<i16x4*>(pb) = rb;
+  lds_st(L, pa, ra);
+  lds_st(L, pb, rb);
 }
 
-// Block id -> (chunk, head group). Head groups of one chunk sit 8 ids apart
-// (same XCD under round-robin dispatch, consecutive dispatch rounds).
+// Block id -> (chunk, head group).
 __device__ inline void block_coords(int groups, int* chunk, int* group) {
   const int id = blockIdx.x;
+  if (groups == 1) {
+    *chunk = id;
+    *group = 0;
+    return;
+  }
   const int x = id & 7, k = id >> 3;
   *group = k % groups;
   *chunk = (k / groups) * 8 + x;
@@ -201,27 +284,15 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
   typedef typename O_::vec vec;
   typedef typename O_::elem E;
 
-  extern __shared__ __attribute__((aligned(1024))) char lds[];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
+  lchar* L = (lchar*)lds_raw;
+  const int tid = threadIdx.x, lane0 = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keep in SGPRs
   int chunk, group;
   block_coords(groups, &chunk, &group);
   if (chunk >= p.num_chunks) return;
   const int hg_heads = min(kHG, p.Hq - group * kHG);
-  const int hb = wave & 3;                  // QK head block (16 heads)
-  const int nbq = wave >> 2;                // QK position half (16 positions)
-  const bool qk_wave = hb * 16 < hg_heads;
-
-  char* pbuf = lds + kPOff;
-  float* alpha_s = reinterpret_cast<float*>(lds + kAlphaOff);
-  float* tmax_s = reinterpret_cast<float*>(lds + kTmaxOff);
-  float* lsum_s = reinterpret_cast<float*>(lds + kLsumOff);
-  float* invl_s = reinterpret_cast<float*>(lds + kInvLOff);
-  // Heads without a query keep P = 0, alpha = 1, 1/l = 0 for the whole block.
-  for (int i = tid; i < kHG * kPRowBytes / 4; i += kThreads) reinterpret_cast<float*>(pbuf)[i] = 0.f;
-  for (int i = tid; i < kHG; i += kThreads) {
-    alpha_s[i] = 1.f;
-    invl_s[i] = 0.f;
-  }
+  const uint32_t scratch = kScratchOff + 128 * wave;  // per-wave 32 floats
 
   const int64_t end_all = seq_begin(p, p.num_seqs);
   int64_t lo = (int64_t)chunk * p.chunk_len;
@@ -230,224 +301,254 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
   if (lo >= hi) return;
   int s = find_seq(p, lo);
 
-  const int l16 = lane & 15, g16 = lane >> 4;
-
   while (lo < hi) {
     const int64_t s_lo = seq_begin(p, s), s_hi = seq_begin(p, s + 1);
     if (s_hi <= lo) {
       ++s;
       continue;
     }
+    const int64_t seg_hi = min(hi, s_hi);
     SegCtx sg;
-    sg.base = reinterpret_cast<const char*>(p.kv) + lo * kRowBytes;
-    sg.seg_lo = lo;
-    sg.seg_hi = min(hi, s_hi);
+    sg.base = reinterpret_cast<const char*>(p.kv) + lo * (kDc + kDr) * 2;
     sg.pos0 = lo - s_lo;
-    sg.last = (int)(sg.seg_hi - sg.seg_lo - 1);
-    const int ntiles = (int)((sg.seg_hi - sg.seg_lo + kT - 1) / kT);
+    sg.last = (int)(seg_hi - lo - 1);
+    const int seg_len = sg.last + 1;
+    const int ntiles = (seg_len + kT - 1) / kT;
 
-    lds_barrier();  // previous segment (or the init above) is done with LDS
+    lds_barrier();  // all waves are done with the previous segment's buffers
 
-    // ---- prologue: tiles 0 and 1 in flight, Q into registers ----
-    issue_tile_dma(p, sg, 0, lds + 0 * kBufBytes, wave, lane);
-    if (ntiles > 1) issue_tile_dma(p, sg, 1, lds + 1 * kBufBytes, wave, lane);
+    issue_tile_dma(p, sg, 0, L, 0, wave, lane0);
+    if (ntiles > 1) issue_tile_dma(p, sg, 1, L, kBufBytes, wave, lane0);
 
-    vec qa[18];
-    if (qk_wave) {
-      const int64_t qhead = (int64_t)s * p.Hq + group * kHG + hb * 16 + l16;
-      const float* qsrc = p.q_abs + qhead * kDc + 8 * g16;
-      const float* rsrc = p.q_rope + qhead * kDr + 8 * g16;
+    // Q^T as the B operand: lane holds Q[head][16kk + 8*g2 .. +8], pre-scaled.
+    // The 32 latent k-steps stay in VGPRs; the 4 rope k-steps go to this
+    // wave's rows of an LDS table (row = head, 16-B chunk j at j ^ (head & 7))
+    // to save 16 VGPRs.
+    vec qb[32];
+    {
+      const int g2 = lane0 >> 5;
+      const int head = 32 * wave + (lane0 & 31);
+      const bool head_ok = head < hg_heads;
+      const int64_t qrow = (int64_t)s * p.Hq + group * kHG + (head_ok ? head : 0);
+      const float* qsrc = p.q_abs + qrow * kDc + 8 * g2;
+      const float* rsrc = p.q_rope + qrow * kDr + 8 * g2;
+      const float sc = head_ok ? p.scale_log2 : 0.f;
 #pragma unroll
-      for (int kk = 0; kk < 18; ++kk) {
-        const float* src = kk < 16 ? qsrc + 32 * kk : rsrc + 32 * (kk - 16);
+      for (int kk = 0; kk < 36; ++kk) {
+        const float* src = kk < 32 ? qsrc + 16 * kk : rsrc + 16 * (kk - 32);
         const f32x4 a = *reinterpret_cast<const f32x4*>(src);
         const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
         vec v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[e] = (E)(a[e] * p.scale_log2);
-          v[4 + e] = (E)(b[e] * p.scale_log2);
+          v[e] = (E)(a[e] * sc);
+          v[4 + e] = (E)(b[e] * sc);
         }
-        qa[kk] = v;
+        if (kk < 32) {
+          qb[kk] = v;
+        } else {
+          const int j = 2 * (kk - 32) + g2;
+          lds_st(L, kQropeOff + head * 128 + ((j ^ (head & 7)) << 4), v);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // bound the loads in flight (register pressure)
       }
     }
 
-    float m_run[4], l_run[4];
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x16 acc[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      m_run[i] = -INFINITY;
-      l_run[i] = 0.f;
-    }
-    f32x16 acc[kNHB][2];
+    for (int nb = 0; nb < 16; ++nb)
 #pragma unroll
-    for (int mb = 0; mb < kNHB; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[mb][nb][e] = 0.f;
+      for (int e = 0; e < 16; ++e) acc[nb][e] = 0.f;
+    acc_ready(acc);
 
-    wait_vm0();
-    lds_barrier();
-    rotate_tile<KT>(lds + 0 * kBufBytes, tid);
-    if (ntiles > 1) rotate_tile<KT>(lds + 1 * kBufBytes, tid);
-    lds_barrier();
+    wait_vm<0>();
+    rotate_rows<KT>(L, 0, wave, lane0);
+    if (ntiles > 1) rotate_rows<KT>(L, kBufBytes, wave, lane0);
 
     for (int t = 0; t < ntiles; ++t) {
-      char* cur = lds + (t % kNBuf) * kBufBytes;
-      const int64_t trow0 = sg.seg_lo + (int64_t)t * kT;
-      const int hrow = hb * 16 + 4 * g16;  // first of this lane's 4 heads (QK layout)
+      lds_barrier();  // tile t staged and rotated by every wave; tile t-1 fully consumed
+      const int lane = opaque(tid & 63);
+      const int g2 = lane >> 5;
+      const int q16 = lane >> 4, s16 = lane & 15;
+      const int head = 32 * wave + (lane & 31);
+      if (t + 2 < ntiles) issue_tile_dma(p, sg, t + 2, L, ((t + 2) % kNBuf) * kBufBytes, wave, lane);
+      const uint32_t cur = (t % kNBuf) * kBufBytes;
 
-      // ---- scores: 16 heads x 16 positions per wave ----
-      // Row brow, logical chunk 4kk + g16 sits at physical chunk
-      // 8(kk>>1) + ((4(kk&1) + g16) ^ (brow&7)): two lane bases (kk even/odd)
-      // plus compile-time offsets 128(kk>>1).
-      f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-      if (qk_wave) {
-        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-        const int brow = 16 * nbq + l16;
-        const char* be = cur + brow * kRowBytes + ((g16 ^ (brow & 7)) << 4);
-        const char* bo = cur + brow * kRowBytes + (((4 + g16) ^ (brow & 7)) << 4);
+      // ---- S^T[pos][head] over 36 k-steps (32 latent + 4 rope) ----
+      // A operand of k-step kk: row arow, logical chunk 2kk + g2, stored at
+      // 2(kk ^ (af>>1)) + (g2 ^ (af&1)). For kk = 4m + r that is byte offset
+      // 128m + 32(r ^ (af>>1)) + 16(g2 ^ (af&1)). A operands are prefetched two
+      // k-steps ahead.
+      const int arow = lane & 31;
+      const int af = swzf(arow & 7);
+      const uint32_t ct_row = cur + arow * 1024 + 16 * (g2 ^ (af & 1));
+      const uint32_t rp_row = cur + kRopeOff + arow * 128 + 16 * (g2 ^ (af & 1));
+      auto a_off = [&](int kk) -> uint32_t {
+        const uint32_t o = 32 * ((kk & 3) ^ (af >> 1)) + 128 * (kk >> 2);
+        return kk < 32 ? ct_row + o : rp_row + o - 128 * 8;
+      };
+      const uint32_t qr_row = kQropeOff + head * 128;
+      // two independent accumulation chains (even / odd k-steps)
+      f32x16 s0, s1;
+      vec an0 = lds_ld<vec>(L, a_off(0)), an1 = lds_ld<vec>(L, a_off(1));
 #pragma unroll
-        for (int kk = 0; kk < 18; kk += 2) {
-          const vec b0 = lds_load<vec>(be, 128 * (kk >> 1));
-          const vec b1 = lds_load<vec>(bo, 128 * (kk >> 1));
-          s0 = O_::mma16(qa[kk], b0, s0);
-          s1 = O_::mma16(qa[kk + 1], b1, s1);
+      for (int kk = 0; kk < 36; kk += 2) {
+        const vec a0 = an0, a1 = an1;
+        if (kk + 2 < 36) {
+          an0 = lds_ld<vec>(L, a_off(kk + 2));
+          an1 = lds_ld<vec>(L, a_off(kk + 3));
         }
-        sc = s0 + s1;
-        const bool valid = trow0 + brow < sg.seg_hi;
-        float mx[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sc[i] = valid ? sc[i] : -INFINITY;
-          float v = sc[i];
-          v = fmaxf(v, __shfl_xor(v, 1, 64));
-          v = fmaxf(v, __shfl_xor(v, 2, 64));
-          v = fmaxf(v, __shfl_xor(v, 4, 64));
-          v = fmaxf(v, __shfl_xor(v, 8, 64));
-          mx[i] = v;
+        if (kk == 0) {
+          O_::mma_v0(s0, a0, qb[0]);
+          O_::mma_v0(s1, a1, qb[1]);
+        } else if (kk < 32) {
+          O_::mma_v(s0, a0, qb[kk]);
+          O_::mma_v(s1, a1, qb[kk + 1]);
+        } else {
+          const vec b0 = lds_ld<vec>(L, qr_row + (((2 * (kk - 32) + g2) ^ (head & 7)) << 4));
+          const vec b1 = lds_ld<vec>(L, qr_row + (((2 * (kk - 31) + g2) ^ (head & 7)) << 4));
+          O_::mma_v(s0, a0, b0);
+          O_::mma_v(s1, a1, b1);
         }
-        if (l16 == 0) *reinterpret_cast<f32x4*>(tmax_s + nbq * kHG + hrow) = f32x4{mx[0], mx[1], mx[2], mx[3]};
       }
-      lds_barrier();  // both position halves' tile maxima visible
+      settle(s0, s1);
+      f32x16 sc = s0 + s1;
 
-      if (qk_wave) {
-        const f32x4 mo = *reinterpret_cast<const f32x4*>(tmax_s + (1 - nbq) * kHG + hrow);
-        const f32x4 mm = *reinterpret_cast<const f32x4*>(tmax_s + nbq * kHG + hrow);
-        float alpha[4];
+      // ---- lazy online softmax; lane = head, 16 positions 8(i/4)+4*g2+(i%4) ----
+      const int valid = min(kT, seg_len - t * kT);
+      float lmax = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float m_new = fmaxf(m_run[i], fmaxf(mm[i], mo[i]));
-          alpha[i] = m_run[i] == -INFINITY ? 0.f : exp2f(m_run[i] - m_new);
-          const E pe = (E)exp2f(sc[i] - m_new);
-          *reinterpret_cast<E*>(pbuf + (hrow + i) * kPRowBytes + (16 * nbq + l16) * 2) = pe;
-          float ts = (float)pe;
-          ts += __shfl_xor(ts, 1, 64);
-          ts += __shfl_xor(ts, 2, 64);
-          ts += __shfl_xor(ts, 4, 64);
-          ts += __shfl_xor(ts, 8, 64);
-          l_run[i] = l_run[i] * alpha[i] + ts;
-          m_run[i] = m_new;
-        }
-        if (nbq == 0 && l16 == 0)
-          *reinterpret_cast<f32x4*>(alpha_s + hrow) = f32x4{alpha[0], alpha[1], alpha[2], alpha[3]};
+      for (int i = 0; i < 16; ++i) {
+        const int pos = 8 * (i >> 2) + 4 * g2 + (i & 3);
+        sc[i] = pos < valid ? sc[i] : -INFINITY;
+        lmax = fmaxf(lmax, sc[i]);
       }
-
-      wait_vm0();     // this wave's copies of tile t+1 have landed
-      lds_barrier();  // P/alpha of tile t visible; tile t+1 complete; PV(t-1) done
-
-      if (t + 2 < ntiles) issue_tile_dma(p, sg, t + 2, lds + ((t + 2) % kNBuf) * kBufBytes, wave, lane);
-      if (t >= 1 && t + 1 < ntiles) rotate_tile<KT>(lds + ((t + 1) % kNBuf) * kBufBytes, tid);
-
-      // ---- O[:, 64w : 64w+64] = alpha * O + P . tile ----
+      const bool need = lmax > m_run + (float)kRescaleSlack;
+      if (__builtin_amdgcn_ballot_w64(need) != 0) {
+        const float tmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
+        const float m_new = fmaxf(m_run, tmax);
+        const bool first = m_run == -INFINITY;
+        const float alpha = first ? 0.f : exp2f(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+        // O rows are heads 8(i/4) + 4*g2 + (i%4); alpha of head h sits in lane h.
+        if (__builtin_amdgcn_ballot_w64(!first && alpha != 1.f) != 0) {
+          if (lane < 32) lds_st(L, scratch + 4 * lane, alpha);
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): own LDS write before own read
+          settle_acc(acc);
+          f32x16 a16;
 #pragma unroll
-      for (int mb = 0; mb < kNHB; ++mb) {
+          for (int q = 0; q < 4; ++q) {
+            const f32x4 a4 = lds_ld<f32x4>(L, scratch + 4 * (8 * q + 4 * g2));
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f32x4 a4 = *reinterpret_cast<const f32x4*>(alpha_s + 32 * mb + 8 * q + 4 * (lane >> 5));
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            acc[mb][0][4 * q + r] *= a4[r];
-            acc[mb][1][4 * q + r] *= a4[r];
+            for (int r = 0; r < 4; ++r) a16[4 * q + r] = a4[r];
           }
+          // one 16-register block at a time, pinned back to AGPRs after each,
+          // so the rescale needs 16 temporaries instead of 256
+#pragma unroll
+          for (int nb = 0; nb < 16; ++nb) {
+            acc[nb] *= a16;
+            pin_agpr(acc[nb]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          acc_ready(acc);
         }
       }
-      // B operand rows 16ks + 8(g16>>1) + 4hf + (l16>>2), logical chunk
-      // 8w + 4nb + 2(g16&1) + ((l16&3)>>1); row&7 = 4hf + (l16>>2), so the
-      // physical chunk is 8w + ((4nb + 2(g16&1) + ((l16&3)>>1)) ^ (4hf + (l16>>2))).
-      const char* trb[2][2];
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int row = 8 * (g16 >> 1) + 4 * hf + (l16 >> 2);
-          const int pj = 8 * wave + ((4 * nb + 2 * (g16 & 1) + ((l16 & 3) >> 1)) ^ (4 * hf + (l16 >> 2)));
-          trb[nb][hf] = cur + row * kRowBytes + pj * 16 + 8 * (l16 & 1);
-        }
-      const char* pa = pbuf + (lane & 31) * kPRowBytes + 16 * (lane >> 5);
+      vec pv[2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        vec bv[2];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          i16x8 v;
-#pragma unroll
-          for (int hf = 0; hf < 2; ++hf) {
-            const i16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) i16x4*)(lds_void*)(trb[nb][hf] + 16 * ks * kRowBytes));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[4 * hf + e] = x[e];
-          }
-          bv[nb] = __builtin_bit_cast(vec, v);
-        }
-#pragma unroll
-        for (int mb = 0; mb < kNHB; ++mb) {
-          const vec av = lds_load<vec>(pa, 32 * mb * kPRowBytes + 32 * ks);
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = O_::mma32(av, bv[nb], acc[mb][nb]);
+        for (int j = 0; j < 8; ++j) {
+          const E pe = (E)exp2f(sc[8 * ks + j] - m_run);
+          pv[ks][j] = pe;
+          l_run += (float)pe;
         }
       }
-      lds_barrier();  // PV(t) done with P; rotation of tile t+1 visible
+      operands_ready(pv[0], pv[1]);
+
+      // ---- O[head][c] += P[head][pos] . tile[pos][c], 16 column blocks ----
+      // B operand for (ks, nb): rows 16ks + 8hf + 4(q16>>1) + (s16>>2) (row&7
+      // does not depend on ks, hf), logical chunk 4nb + jlo with
+      // jlo = 2(q16&1) + ((s16&3)>>1). With F = swzf(row), the physical chunk is
+      // 4(nb ^ (F>>2)) + (jlo ^ (F&3)): byte offset 64nb +- 64(F>>2) (sign by the
+      // parity of nb) + 16(jlo ^ (F&3)) -- two lane bases plus immediates.
+      const int trow = 4 * (q16 >> 1) + (s16 >> 2);
+      const int tf = swzf(trow);
+      const uint32_t tb = cur + trow * 1024 + 16 * ((2 * (q16 & 1) + ((s16 & 3) >> 1)) ^ (tf & 3)) + 8 * (s16 & 1);
+      const uint32_t tb_even = tb + 64 * (tf >> 2);
+      const uint32_t tb_odd = tb - 64 * (tf >> 2);
+      // The two transposed reads of step s+1 are issued before the MFMA of
+      // step s; lgkmcnt(2) then guarantees everything older than them (the
+      // reads of step s) has landed (LDS operations complete in order). The
+      // wait takes the raw read registers as operands so nothing copies them
+      // earlier.
+      auto b_issue = [&](int step) -> TrPair {
+        const int ks = step >> 4, nb = step & 15;
+        const uint32_t base = ((nb & 1) ? tb_odd : tb_even) + 64 * nb;
+        TrPair r;
+        r.x0 = lds_tr(L, base + (16 * ks) * 1024);
+        r.x1 = lds_tr(L, base + (16 * ks + 8) * 1024);
+        return r;
+      };
+      TrPair bn = b_issue(0);
+#pragma unroll
+      for (int step = 0; step < 32; ++step) {
+        TrPair bc = bn;
+        if (step + 1 < 32) {
+          bn = b_issue(step + 1);
+          asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(bc.x0), "+v"(bc.x1));
+        } else {
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(bc.x0), "+v"(bc.x1));
+        }
+        i16x8 bv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          bv[e] = bc.x0[e];
+          bv[4 + e] = bc.x1[e];
+        }
+        O_::mma_a(acc[step & 15], pv[step >> 4], __builtin_bit_cast(vec, bv));
+      }
+
+      if (t + 1 < ntiles && t >= 1) {
+        if (t + 2 < ntiles) wait_vm<kDmaPerWave>();
+        else wait_vm<0>();
+        rotate_rows<KT>(L, ((t + 1) % kNBuf) * kBufBytes, wave, lane);
+      }
     }
 
-    // ---- segment end: l = l(half 0) + l(half 1); normalise; write the slot ----
+    // ---- segment end: l over both lane halves; normalise; write the slot ----
+    settle_acc(acc);
+    const int g2 = lane0 >> 5;
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
     const int64_t slot = (int64_t)chunk + s;
-    const int hrow = hb * 16 + 4 * g16;
-    if (qk_wave && l16 == 0)
-      *reinterpret_cast<f32x4*>(lsum_s + nbq * kHG + hrow) = f32x4{l_run[0], l_run[1], l_run[2], l_run[3]};
-    lds_barrier();
-    if (qk_wave && nbq == 0 && l16 == 0) {
-      const f32x4 l0 = *reinterpret_cast<const f32x4*>(lsum_s + hrow);
-      const f32x4 l1 = *reinterpret_cast<const f32x4*>(lsum_s + kHG + hrow);
-      f32x4 il;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float lt = l0[i] + l1[i];
-        il[i] = 1.f / lt;
-        p.part_lse[slot * p.Hq + group * kHG + hrow + i] = m_run[i] + log2f(lt);
-      }
-      *reinterpret_cast<f32x4*>(invl_s + hrow) = il;
+    const int64_t hq0 = slot * p.Hq + group * kHG + 32 * wave;
+    if (lane0 < 32) {
+      lds_st(L, scratch + 4 * lane0, 1.f / l_tot);
+      if (32 * wave + lane0 < hg_heads) p.part_lse[hq0 + lane0] = m_run + log2f(l_tot);
     }
-    lds_barrier();
-    // head h = 32mb + 8q + 4(lane>>5) + r lies in 16-head block 2mb + (q>>1);
-    // hg_heads is a multiple of 16, so validity is uniform per (mb, q).
-    float* dst0 = p.part_o + (slot * p.Hq + group * kHG + 4 * (lane >> 5)) * kDc + 64 * wave + (lane & 31);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    f32x16 il16;
 #pragma unroll
-    for (int mb = 0; mb < kNHB; ++mb) {
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 il = lds_ld<f32x4>(L, scratch + 4 * (8 * q + 4 * g2));
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if ((2 * mb + (q >> 1)) * 16 >= hg_heads) continue;
-        const int hbase = 32 * mb + 8 * q;
-        const f32x4 il = *reinterpret_cast<const f32x4*>(invl_s + hbase + 4 * (lane >> 5));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float* dst = dst0 + (int64_t)(hbase + r) * kDc;
-          dst[0] = acc[mb][0][4 * q + r] * il[r];
-          dst[32] = acc[mb][1][4 * q + r] * il[r];
-        }
-      }
+      for (int r = 0; r < 4; ++r) il16[4 * q + r] = il[r];
     }
-    lo = sg.seg_hi;
+    // register i of block nb: head 8(i/4) + 4*g2 + (i%4), column 32nb + lane%32.
+    // Heads come in 16-aligned groups, so validity is uniform per i.
+    float* dst0 = p.part_o + hq0 * kDc + (lane0 & 31);
+#pragma unroll
+    for (int nb = 0; nb < 16; ++nb) {
+      const f32x16 v = acc[nb] * il16;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int hh = 8 * (i >> 2) + 4 * g2 + (i & 3);
+        if (32 * wave + hh < hg_heads) dst0[(int64_t)hh * kDc + 32 * nb] = v[i];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    lo = seg_hi;
     ++s;
   }
 }
@@ -462,7 +563,7 @@ hipError_t launch_t(const DecodeProblem& p, hipStream_t stream) {
     attr_set = true;
   }
   const int groups = (p.Hq + kHG - 1) / kHG;
-  const int64_t blocks = (int64_t)((p.num_chunks + 7) / 8) * 8 * groups;
+  const int64_t blocks = groups == 1 ? p.num_chunks : (int64_t)((p.num_chunks + 7) / 8) * 8 * groups;
   hipLaunchKernelGGL((decode_mfma_kernel<KT>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, stream, p, groups);
   return hipGetLastError();
 }

@@ -1,0 +1,270 @@
+// MFMA kernels for the two small contractions around the attention kernel,
+// for 16-bit weights (bf16 or fp16):
+//
+//   absorb:   q_abs[t,h,c] = sum_i q_nope[t,h,i] * W_UK[h*dn + i, c]
+//             (reference tests/test_correctness.cu:29-46, tests/test_python.py:97-99)
+//   project:  out[t,h,j]   = sum_c O[t,h,c] * W_UV[h*dv + j, c], where O is the
+//             log-sum-exp merge of the split-KV partial slots
+//             (reference src/fused_mla.cu:255-267: normalise, then W_UV)
+//
+// Both run v_mfma_f32_32x32x16 with 32 query tokens as M. The fp32 operand
+// (q_nope, or the merged O) is split into a 16-bit high part and a 16-bit
+// residual (hi = rn(x), lo = rn(x - hi)); two MFMAs accumulate W*hi + W*lo in
+// fp32, so the result keeps ~16 bits of the fp32 operand instead of 8 (bf16)
+// or 11 (fp16). For fp16 the residual is pre-multiplied by 2^11 (and its
+// product by 2^-11) so it stays in the normal range.
+//
+// absorb:  grid (nh, dc/128, ceil(T/32)), 256 threads. W_UK[h][:, 128-col
+//          block] (128 x 128) is staged in LDS; wave w owns 32 columns; the
+//          B operand (8 consecutive rows i per lane) comes from
+//          ds_read_b64_tr_b16.
+// project: grid (nh, ceil(R/32)), 256 threads. Phase 1 merges the partial
+//          slots of 32 query tokens of weight head h into LDS (hi/lo 16-bit);
+//          phase 2: wave w owns 32 output columns j, B operand = 16 contiguous
+//          bytes of a W_UV row read straight from global memory (each weight
+//          element is read once per block).
+#include "la_internal.hpp"
+
+namespace la {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <typename WT>
+struct Mma;
+
+template <>
+struct Mma<__hip_bfloat16> {
+  typedef bf16x8 vec;
+  typedef __bf16 elem;
+  static constexpr float kLoScale = 1.f;
+  static __device__ inline f32x16 mma(vec a, vec b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mma<__half> {
+  typedef f16x8 vec;
+  typedef _Float16 elem;
+  static constexpr float kLoScale = 2048.f;  // 2^11
+  static __device__ inline f32x16 mma(vec a, vec b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// hi/lo split of 8 fp32 values into two 16-bit operand vectors.
+template <typename WT>
+__device__ inline void split8(const float* x, typename Mma<WT>::vec& hi, typename Mma<WT>::vec& lo) {
+  typedef typename Mma<WT>::elem E;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const E h = (E)x[e];
+    hi[e] = h;
+    lo[e] = (E)((x[e] - (float)h) * Mma<WT>::kLoScale);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// absorb
+// ---------------------------------------------------------------------------
+constexpr int kAbsCols = 128;            // columns per block
+constexpr int kAbsRowBytes = 256 + 32;   // 128 x 16-bit + pad: 4 tr rows hit 4 bank groups
+
+template <typename WT>
+__global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restrict__ q_nope, const WT* __restrict__ W,
+                                                          float* __restrict__ q_abs, int tokens, int nh, int dn,
+                                                          int dc) {
+  typedef Mma<WT> M;
+  typedef typename M::vec vec;
+  __shared__ __attribute__((aligned(16))) char wt[128 * kAbsRowBytes];  // dn <= 128 rows
+  const int h = blockIdx.x, cb = blockIdx.y, t0 = blockIdx.z * 32;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+
+  // stage W_UK[h*dn + i][cb*128 + 0..127] for i < dn (16 B per thread-load)
+  for (int q = tid; q < dn * 16; q += 256) {
+    const int i = q >> 4, ch = q & 15;
+    const i16x8 v = *reinterpret_cast<const i16x8*>(W + ((int64_t)h * dn + i) * dc + cb * kAbsCols + ch * 8);
+    *reinterpret_cast<i16x8*>(wt + i * kAbsRowBytes + ch * 16) = v;
+  }
+  __syncthreads();
+
+  const int t = t0 + (lane & 31);
+  const bool tvalid = t < tokens;
+  const float* qrow = q_nope + ((int64_t)(tvalid ? t : 0) * nh + h) * dn;
+  f32x16 acc_hi = {}, acc_lo = {};
+  const int g = lane >> 4, s = lane & 15;
+  for (int ks = 0; ks < dn / 16; ++ks) {
+    float x[8];
+    if (tvalid) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(qrow + 16 * ks + 8 * (lane >> 5));
+      const f32x4 b = *reinterpret_cast<const f32x4*>(qrow + 16 * ks + 8 * (lane >> 5) + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = a[e];
+        x[4 + e] = b[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = 0.f;
+    }
+    vec ahi, alo;
+    split8<WT>(x, ahi, alo);
+    // B[k = i][n = c]: rows 16ks + 8(g>>1) + 4hf + (s>>2), columns 32w + 16(g&1) + 4(s&3)
+    i16x8 bv;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int row = 16 * ks + 8 * (g >> 1) + 4 * hf + (s >> 2);
+      const int col = 32 * wave + 16 * (g & 1) + 4 * (s & 3);
+      const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) i16x4*)(lds_void*)(wt + row * kAbsRowBytes + col * 2));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bv[4 * hf + e] = r[e];
+    }
+    const vec b = __builtin_bit_cast(vec, bv);
+    acc_hi = M::mma(ahi, b, acc_hi);
+    acc_lo = M::mma(alo, b, acc_lo);
+  }
+  // D[m = token][n = column]
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    const int tt = t0 + m;
+    if (tt < tokens)
+      q_abs[((int64_t)tt * nh + h) * dc + cb * kAbsCols + 32 * wave + (lane & 31)] =
+          acc_hi[i] + acc_lo[i] * (1.f / M::kLoScale);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// combine + project
+// ---------------------------------------------------------------------------
+constexpr int kDcP = 512;
+constexpr int kORowBytes = kDcP * 2 + 16;  // 16-bit O row + pad (8 rows -> 8 bank groups)
+constexpr int kProjLdsBytes = 2 * 32 * kORowBytes;
+
+template <typename WT>
+__global__ __launch_bounds__(256) void combine_project_mfma_kernel(DecodeProblem p) {
+  typedef Mma<WT> M;
+  typedef typename M::vec vec;
+  typedef typename M::elem E;
+  extern __shared__ __attribute__((aligned(16))) char o_lds[];  // kProjLdsBytes
+  char* o_hi = o_lds;
+  char* o_lo = o_lds + 32 * kORowBytes;
+  const int h = blockIdx.x, r0 = blockIdx.y * 32;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int R = p.num_seqs * p.qps;
+
+  // ---- phase 1: merge the partial slots of 32 tokens into LDS ----
+  for (int rr = wave; rr < 32; rr += 4) {
+    const int r = r0 + rr;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = 0.f;
+    if (r < R) {
+      const int s = r / p.qps;
+      const int hq = (r % p.qps) * p.nh + h;
+      const int64_t lo = seq_begin(p, s), hi = seq_begin(p, s + 1);
+      if (hi > lo) {
+        const int64_t cf = lo / p.chunk_len, cl = (hi - 1) / p.chunk_len;
+        float mx = -INFINITY;
+        for (int64_t c = cf; c <= cl; ++c) mx = fmaxf(mx, p.part_lse[(c + s) * p.Hq + hq]);
+        float wsum = 0.f;
+        for (int64_t c = cf; c <= cl; ++c) {
+          const int64_t slot = c + s;
+          const float w = exp2f(p.part_lse[slot * p.Hq + hq] - mx);
+          wsum += w;
+          const float* src = p.part_o + (slot * p.Hq + hq) * kDcP + lane * 8;
+          const f32x4 a = *reinterpret_cast<const f32x4*>(src);
+          const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[e] += w * a[e];
+            o[4 + e] += w * b[e];
+          }
+        }
+        const float inv = 1.f / wsum;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] *= inv;
+      }
+    }
+    vec vh, vl;
+    split8<WT>(o, vh, vl);
+    *reinterpret_cast<vec*>(o_hi + rr * kORowBytes + lane * 16) = vh;
+    *reinterpret_cast<vec*>(o_lo + rr * kORowBytes + lane * 16) = vl;
+  }
+  __syncthreads();
+
+  // ---- phase 2: out[token][32w + n] = sum_c O[token][c] * W_UV[h*dv + 32w + n][c] ----
+  const WT* wrow = reinterpret_cast<const WT*>(p.W_UV) + ((int64_t)h * p.dv + 32 * wave + (lane & 31)) * kDcP +
+                   8 * (lane >> 5);
+  const char* ah = o_hi + (lane & 31) * kORowBytes + 16 * (lane >> 5);
+  const char* al = o_lo + (lane & 31) * kORowBytes + 16 * (lane >> 5);
+  f32x16 acc_hi = {}, acc_lo = {};
+#pragma unroll 4
+  for (int ks = 0; ks < kDcP / 16; ++ks) {
+    const vec b = __builtin_bit_cast(vec, *reinterpret_cast<const i16x8*>(wrow + 16 * ks));
+    const vec a1 = *reinterpret_cast<const vec*>(ah + 32 * ks);
+    const vec a2 = *reinterpret_cast<const vec*>(al + 32 * ks);
+    acc_hi = M::mma(a1, b, acc_hi);
+    acc_lo = M::mma(a2, b, acc_lo);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    const int r = r0 + m;
+    if (r < R) p.out[((int64_t)r * p.nh + h) * p.dv + 32 * wave + (lane & 31)] = acc_hi[i] + acc_lo[i] * (1.f / M::kLoScale);
+  }
+}
+
+}  // namespace
+
+bool absorb_mfma_supported(int w_dtype, int nh, int dn, int dc) {
+  (void)nh;
+  return (w_dtype == LA_DTYPE_BF16 || w_dtype == LA_DTYPE_F16) && dn % 16 == 0 && dn <= 128 && dc % kAbsCols == 0;
+}
+
+hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype, float* q_abs, int tokens, int nh,
+                              int dn, int dc, hipStream_t stream) {
+  dim3 grid(nh, dc / kAbsCols, (tokens + 31) / 32);
+  if (w_dtype == LA_DTYPE_BF16)
+    hipLaunchKernelGGL(absorb_mfma_kernel<__hip_bfloat16>, grid, dim3(256), 0, stream, q_nope,
+                       reinterpret_cast<const __hip_bfloat16*>(W_UK), q_abs, tokens, nh, dn, dc);
+  else
+    hipLaunchKernelGGL(absorb_mfma_kernel<__half>, grid, dim3(256), 0, stream, q_nope,
+                       reinterpret_cast<const __half*>(W_UK), q_abs, tokens, nh, dn, dc);
+  return hipGetLastError();
+}
+
+bool project_mfma_supported(const DecodeProblem& p) {
+  return (p.wuv_dtype == LA_DTYPE_BF16 || p.wuv_dtype == LA_DTYPE_F16) && p.dc == kDcP && p.dv % 128 == 0 &&
+         p.dv == 128 && (reinterpret_cast<uintptr_t>(p.W_UV) & 15) == 0;
+}
+
+template <typename WT>
+hipError_t launch_cp(const DecodeProblem& p, hipStream_t stream) {
+  static bool attr_set = false;  // per instance; setting it twice is harmless
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&combine_project_mfma_kernel<WT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kProjLdsBytes);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int R = p.num_seqs * p.qps;
+  dim3 grid(p.nh, (R + 31) / 32);
+  hipLaunchKernelGGL(combine_project_mfma_kernel<WT>, grid, dim3(256), kProjLdsBytes, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine_project_mfma(const DecodeProblem& p, hipStream_t stream) {
+  if (p.wuv_dtype == LA_DTYPE_BF16) return launch_cp<__hip_bfloat16>(p, stream);
+  return launch_cp<__half>(p, stream);
+}
+
+}  // namespace la
