@@ -55,7 +55,7 @@ struct Plan {
   int chunk_len = 0;
   int num_chunks = 0;
   int num_slots = 0;
-  size_t q_abs_off = 0, part_o_off = 0, part_lse_off = 0, total = 0;
+  size_t q_abs_off = 0, q_prep_off = 0, part_o_off = 0, part_lse_off = 0, total = 0;
 };
 
 // Fills the problem (without workspace pointers) and the plan. The args'
@@ -142,6 +142,10 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
     pl.q_abs_off = off;
     off += align_up((size_t)tokens * c.num_heads * c.kv_lora_rank * sizeof(float));
   }
+  if (pl.mfma) {
+    pl.q_prep_off = off;
+    off += align_up((size_t)a->num_seqs * p->Hq * (c.kv_lora_rank + c.qk_rope_head_dim) * 2);
+  }
   pl.part_o_off = off;
   off += align_up((size_t)pl.num_slots * p->Hq * c.kv_lora_rank * sizeof(float));
   pl.part_lse_off = off;
@@ -200,6 +204,12 @@ int run(const la_decode_args* a, hipStream_t stream) {
   p.part_o = reinterpret_cast<float*>(ws + plan.part_o_off);
   p.part_lse = reinterpret_cast<float*>(ws + plan.part_lse_off);
   if (plan.num_chunks > 0) {
+    if (plan.mfma) {
+      p.q_prep = ws + plan.q_prep_off;
+      hipError_t e = launch_prep_q(p, stream);
+      if (e != hipSuccess) return finish(e);
+    }
+    // the optional events bracket the attention kernel alone
     if (a->decode_event_begin) {
       hipError_t e = hipEventRecord(static_cast<hipEvent_t>(a->decode_event_begin), stream);
       if (e != hipSuccess) return finish(e);

@@ -40,6 +40,8 @@ struct DecodeProblem {
   int Hq;                 // query heads per sequence = qps * nh
   const float* q_abs;     // (num_seqs*Hq, dc) f32
   const float* q_rope;    // (num_seqs*Hq, dR) f32
+  void* q_prep;           // MFMA path: (num_seqs*Hq, dc + dR) in the cache's 16-bit type,
+                          // [q_abs | q_rope] * scale_log2, written by launch_prep_q
   const void* W_UV;
   int wuv_dtype;
   const float* rope_cos;
@@ -122,6 +124,8 @@ hipError_t launch_decode_mfma(const DecodeProblem& p, hipStream_t stream);
 bool mfma_supported(const DecodeProblem& p);
 int mfma_heads_per_group();
 int mfma_max_chunk_rows();
+// Fills p.q_prep from p.q_abs and p.q_rope (MFMA path only).
+hipError_t launch_prep_q(const DecodeProblem& p, hipStream_t stream);
 
 // log-sum-exp combine of the partial slots + W_UV projection into p.out.
 hipError_t launch_combine_project(const DecodeProblem& p, hipStream_t stream);

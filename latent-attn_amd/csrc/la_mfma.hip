@@ -19,9 +19,11 @@
 //   * Staging: per tile, wave w copies rows 8w..8w+7 HBM->LDS with
 //     global_load_lds_dwordx4 (c_t rows, k_rope rows, cos and sin rows: 11
 //     copies per wave, no VGPR staging) into a 3-deep ring, two tiles ahead.
-//     Inside a row the 16-B chunk j lives at chunk j ^ f(row),
-//     f(row) = 2(row&3) | ((row>>2)&1): 8 consecutive rows at one column and
-//     4 consecutive rows at two adjacent columns both land in distinct banks.
+//     Inside a c_t row the 16-B chunk j lives at chunk j ^ fc(row),
+//     fc(row) = 4(row&3) | ((row>>2)&3); inside a k_rope row at j ^ fr(row),
+//     fr(row) = (row>>1)&7. With 64 banks of 4 B this makes both the score
+//     reads (16 rows at one column per 16 lanes) and the transposed value
+//     reads (4 rows x 4 columns per 16 lanes) conflict-free.
 //     Each wave rotates (RoPE) the k_rope rows it copied itself, so only its
 //     own vmcnt has to drain; one s_barrier per tile publishes the tile.
 //   * Scores: S^T[32 pos x 32 heads] = sum over 36 k-steps of
@@ -41,6 +43,7 @@
 
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 
 namespace la {
 namespace {
@@ -62,6 +65,51 @@ constexpr int kQropeOff = kScratchOff + kWaves * 32 * 4;  // q_rope of the group
 constexpr int kLdsBytes = kQropeOff + kHG * kDr * 2;
 constexpr int kDmaPerWave = 11;        // 8 c_t rows + k_rope + cos + sin
 constexpr int kRescaleSlack = 8;       // log2 units before the running max moves
+constexpr int kQkDepth = 8;            // score A operands read this many k-steps ahead
+constexpr int kPvDepth = 7;            // value reads this many PV steps ahead (2 per step, lgkmcnt <= 15)
+constexpr int kRotStep = 27;           // PV step after which the RoPE reads of tile t+2 are issued
+constexpr int kQrAt = 32 - kQkDepth;   // QK step before which the q_rope table reads are issued
+constexpr int kTrAt = 36 - kPvDepth;   // QK steps kTrAt.. issue the first kPvDepth PV value-read pairs
+constexpr int kSmAt0 = 1, kSmAt1 = 4, kSmAt2 = 8, kSmAt3 = 14;  // softmax pieces after these QK steps
+
+// LDS issue order of one iteration (all reads counted by lgkmcnt):
+//   QK:  A(0..D-1); per step kk: [kk == kQrAt: 4 q_rope reads] wait A(kk),
+//        MFMA, A(kk+D), [kk >= kTrAt: value-read pair kk-kTrAt];
+//   PV:  per step s: wait pair s, MFMA, pair s+kPvDepth, [s == kRotStep: 4
+//        RoPE reads].
+// qk_later(kk) / pv_later(s) = LDS reads issued after the awaited one and
+// before its wait; lgkmcnt(that) then guarantees it has completed.
+constexpr int qk_later(int kk) {
+  const int D = kQkDepth;
+  int seq = 0, seq_a = -1;
+  for (int j = 0; j < D; ++j) {
+    if (j == kk) seq_a = seq;
+    ++seq;
+  }
+  for (int k = 0; k <= kk; ++k) {
+    if (k == kQrAt) seq += 4;
+    if (k == kk) return seq - seq_a - 1;
+    if (k + D < 36) {
+      if (k + D == kk) seq_a = seq;
+      ++seq;
+    }
+    if (k >= kTrAt && k - kTrAt < kPvDepth) seq += 2;
+  }
+  return -1;
+}
+constexpr int pv_later(int s) {
+  // pairs 0..kPvDepth-1 were issued at the end of QK, back to back
+  int seq = 2 * kPvDepth, seq_s = s < kPvDepth ? 2 * s : -1;
+  for (int k = 0; k <= s; ++k) {
+    if (k == s) return seq - seq_s - 2;
+    if (k + kPvDepth < 32) {
+      if (k + kPvDepth == s) seq_s = seq;
+      seq += 2;
+    }
+    if (k == kRotStep) seq += 4;
+  }
+  return -1;
+}
 // Longest chunk the kernel accepts: keeps row byte offsets inside 32 bits.
 constexpr int kMaxChunkRows = 1 << 20;
 
@@ -156,7 +204,10 @@ __device__ inline void acc_ready(f32x16 (&acc)[16]) {
                "+a"(acc[13]), "+a"(acc[14]), "+a"(acc[15]));
 }
 
-__device__ inline int swzf(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+// Chunk swizzles of c_t rows (64 chunks of 16 B) and of 128-B rows (k_rope,
+// the q_rope table): logical chunk j is stored at chunk j ^ f(row).
+__device__ inline int fc(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
+__device__ inline int fr(int row) { return (row >> 1) & 7; }
 
 // vmcnt(n) with the other counters left alone (gfx9 encoding, n < 16).
 template <int N>
@@ -191,13 +242,58 @@ __device__ inline void lds_st(lchar* L, uint32_t off, T v) {
   *reinterpret_cast<__attribute__((address_space(3))) T*>(L + off) = v;
 }
 // ds_read_b64_tr_b16 as inline asm: the builtin makes the compiler assume the
-// read may alias the in-flight HBM->LDS copies and drain vmcnt before it. The
-// asm result must not be used before b_wait() (lgkmcnt).
+// read may alias the in-flight HBM->LDS copies and drain vmcnt before it. OFF
+// is the instruction's immediate byte offset. The result must not be used
+// before an lgkmcnt wait that covers it.
+template <int OFF>
 __device__ inline i16x4 lds_tr(const lchar* L, uint32_t off) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
   i16x4 r;
   const uint32_t addr = (uint32_t)(uintptr_t)(L + off);
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
   return r;
+}
+
+// ds_read_b128 as inline asm, for the same reason; same contract as lds_tr.
+template <typename V>
+__device__ inline V lds_rd128(const lchar* L, uint32_t off) {
+  V r;
+  const uint32_t addr = (uint32_t)(uintptr_t)(L + off);
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+
+__device__ inline i16x4 lds_rd64(const lchar* L, uint32_t off) {
+  i16x4 r;
+  const uint32_t addr = (uint32_t)(uintptr_t)(L + off);
+  asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+
+// lgkmcnt(N) as inline asm whose operands are the registers it protects, so
+// no copy of them is scheduled before the wait.
+template <int N>
+__device__ inline void wait_lgkm(i16x4& a, i16x4& b) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N));
+}
+template <int N, typename V>
+__device__ inline void wait_lgkm(V& a) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "n"(N));
+}
+
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1.
+template <int I, int N, typename F>
+__device__ inline void static_for_impl(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>());
+    static_for_impl<I + 1, N>(f);
+  }
+}
+template <int N, typename F>
+__device__ inline void static_for(F&& f) {
+  static_for_impl<0, N>(f);
 }
 
 struct TrPair {
@@ -210,59 +306,91 @@ struct SegCtx {
   int last;          // index of the segment's last row, relative to its first
 };
 
-// Wave w's 11 HBM->LDS copies for tile k into the buffer at LDS offset buf:
-// c_t of rows 8w..8w+7 (one copy per row), then their k_rope, cos and sin rows
-// (one copy each). Global addresses are a wave-uniform base plus a 32-bit lane
-// offset (segments are capped at kMaxChunkRows rows, tables at 2^24 rows).
-// Rows past the segment end re-read its last row; their scores are masked.
-__device__ inline void issue_tile_dma(const DecodeProblem& p, const SegCtx& sg, int k, lchar* L, uint32_t buf,
-                                      int wave, int lane) {
+// Wave w's HBM->LDS copy J (0..10) of tile k into the buffer at LDS offset
+// buf: J < 8 is the c_t row 8w+J, J = 8 the k_rope rows 8w..8w+7, J = 9 / 10
+// their cos / sin rows. Lane i writes LDS chunk i and fetches the logical
+// chunk that belongs there (i ^ swizzle). Global addresses are a wave-uniform
+// base plus a 32-bit lane offset (segments are capped at kMaxChunkRows rows,
+// tables at 2^24 rows). Rows past the segment end re-read its last row; their
+// scores are masked.
+template <int J>
+__device__ inline void issue_copy(const DecodeProblem& p, const SegCtx& sg, int k, lchar* L, uint32_t buf, int wave,
+                                  int lane) {
   const int r_first = 8 * wave;
-#pragma unroll
-  for (int rr = 0; rr < 8; ++rr) {
-    const int row = r_first + rr;
+  if constexpr (J < 8) {
+    const int row = r_first + J;
     const int r = min(k * kT + row, sg.last);
-    const int j = lane ^ swzf(rr);  // row & 7 == rr
+    const int j = lane ^ fc(row);
     __builtin_amdgcn_global_load_lds(sg.base + (uint32_t)(r * (kDc + kDr) * 2 + j * 16),
                                      (lds_void*)(L + buf + row * 1024), 16, 0, 0);
+  } else {
+    const int row = r_first + (lane >> 3);
+    const int r = min(k * kT + row, sg.last);
+    if constexpr (J == 8) {
+      const int jr = (lane & 7) ^ fr(row);
+      __builtin_amdgcn_global_load_lds(sg.base + (uint32_t)(r * (kDc + kDr) * 2 + kDc * 2 + jr * 16),
+                                       (lds_void*)(L + buf + kRopeOff + r_first * 128), 16, 0, 0);
+    } else {
+      const uint32_t toff = (uint32_t)(rope_row(p, sg.pos0 + r) * (kDr / 2) * 4 + (lane & 7) * 16);
+      const float* tab = J == 9 ? p.rope_cos : p.rope_sin;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(tab) + toff,
+                                       (lds_void*)(L + buf + (J == 9 ? kCosOff : kSinOff) + r_first * 128), 16, 0,
+                                       0);
+    }
   }
-  const int row = r_first + (lane >> 3);
-  const int r = min(k * kT + row, sg.last);
-  const int jr = (lane & 7) ^ swzf(lane >> 3);  // row & 7 == lane >> 3
-  __builtin_amdgcn_global_load_lds(sg.base + (uint32_t)(r * (kDc + kDr) * 2 + kDc * 2 + jr * 16),
-                                   (lds_void*)(L + buf + kRopeOff + r_first * 128), 16, 0, 0);
-  const uint32_t toff = (uint32_t)(rope_row(p, sg.pos0 + r) * (kDr / 2) * 4 + (lane & 7) * 16);
-  __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(p.rope_cos) + toff,
-                                   (lds_void*)(L + buf + kCosOff + r_first * 128), 16, 0, 0);
-  __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(p.rope_sin) + toff,
-                                   (lds_void*)(L + buf + kSinOff + r_first * 128), 16, 0, 0);
+}
+
+// All kDmaPerWave copies of tile k.
+__device__ inline void issue_tile_dma(const DecodeProblem& p, const SegCtx& sg, int k, lchar* L, uint32_t buf,
+                                      int wave, int lane) {
+  static_for<kDmaPerWave>([&](auto j) { issue_copy<decltype(j)::value>(p, sg, k, L, buf, wave, lane); });
 }
 
 // Rotate-half RoPE of rows 8w..8w+7 of the tile at LDS offset buf, in place
 // (src/fused_mla.cu:43-51): r[i] = k[i]*c - k[i+32]*s, r[i+32] = k[i]*s +
-// k[i+32]*c. Lane: row 8w + lane/8, pairs i = 4(lane%8) .. +3.
-template <typename KT>
-__device__ inline void rotate_rows(lchar* L, uint32_t buf, int wave, int lane) {
-  typedef typename Ops<KT>::elem E;
+// k[i+32]*c. Lane: row 8w + lane/8, pairs i = 4(lane%8) .. +3. Split in two:
+// rot_issue starts the four LDS reads (inline asm; the caller waits for them
+// with lgkmcnt), rot_finish rotates and stores.
+struct RotIn {
+  i16x4 ka, kb;
+  f32x4 c, s;
+  uint32_t pa, pb;
+};
+
+__device__ inline RotIn rot_issue(const lchar* L, uint32_t buf, int wave, int lane) {
   const int rl = lane >> 3, u = lane & 7;
   const int row = 8 * wave + rl;
-  const int f = swzf(rl);
-  const uint32_t pa = buf + kRopeOff + row * 128 + (((u >> 1) ^ f) << 4) + 8 * (u & 1);
-  const uint32_t pb = buf + kRopeOff + row * 128 + (((4 + (u >> 1)) ^ f) << 4) + 8 * (u & 1);
-  const i16x4 ka = lds_ld<i16x4>(L, pa);
-  const i16x4 kb = lds_ld<i16x4>(L, pb);
-  const f32x4 c = lds_ld<f32x4>(L, buf + kCosOff + row * 128 + 16 * u);
-  const f32x4 s = lds_ld<f32x4>(L, buf + kSinOff + row * 128 + 16 * u);
+  const int f = fr(row);
+  RotIn r;
+  r.pa = buf + kRopeOff + row * 128 + (((u >> 1) ^ f) << 4) + 8 * (u & 1);
+  r.pb = buf + kRopeOff + row * 128 + (((4 + (u >> 1)) ^ f) << 4) + 8 * (u & 1);
+  r.ka = lds_rd64(L, r.pa);
+  r.kb = lds_rd64(L, r.pb);
+  r.c = lds_rd128<f32x4>(L, buf + kCosOff + row * 128 + 16 * u);
+  r.s = lds_rd128<f32x4>(L, buf + kSinOff + row * 128 + 16 * u);
+  return r;
+}
+
+template <typename KT>
+__device__ inline void rot_finish(lchar* L, RotIn& in) {
+  typedef typename Ops<KT>::elem E;
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(in.ka), "+v"(in.kb), "+v"(in.c), "+v"(in.s));
   i16x4 ra, rb;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const float k0 = (float)__builtin_bit_cast(E, (short)ka[e]);
-    const float k1 = (float)__builtin_bit_cast(E, (short)kb[e]);
-    ra[e] = __builtin_bit_cast(short, (E)(k0 * c[e] - k1 * s[e]));
-    rb[e] = __builtin_bit_cast(short, (E)(k0 * s[e] + k1 * c[e]));
+    const float k0 = (float)__builtin_bit_cast(E, (short)in.ka[e]);
+    const float k1 = (float)__builtin_bit_cast(E, (short)in.kb[e]);
+    ra[e] = __builtin_bit_cast(short, (E)(k0 * in.c[e] - k1 * in.s[e]));
+    rb[e] = __builtin_bit_cast(short, (E)(k0 * in.s[e] + k1 * in.c[e]));
   }
-  lds_st(L, pa, ra);
-  lds_st(L, pb, rb);
+  lds_st(L, in.pa, ra);
+  lds_st(L, in.pb, rb);
+}
+
+template <typename KT>
+__device__ inline void rotate_rows(lchar* L, uint32_t buf, int wave, int lane) {
+  RotIn r = rot_issue(L, buf, wave, lane);
+  rot_finish<KT>(L, r);
 }
 
 // Block id -> (chunk, head group).
@@ -322,35 +450,32 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
 
     // Q^T as the B operand: lane holds Q[head][16kk + 8*g2 .. +8], pre-scaled.
     // The 32 latent k-steps stay in VGPRs; the 4 rope k-steps go to this
-    // wave's rows of an LDS table (row = head, 16-B chunk j at j ^ (head & 7))
+    // wave's rows of an LDS table (row = head, 16-B chunk j at j ^ fr(head))
     // to save 16 VGPRs.
     vec qb[32];
     {
+      // 16-bit Q rows prepared by prep_q_kernel: all 36 loads go out at once
       const int g2 = lane0 >> 5;
       const int head = 32 * wave + (lane0 & 31);
       const bool head_ok = head < hg_heads;
       const int64_t qrow = (int64_t)s * p.Hq + group * kHG + (head_ok ? head : 0);
-      const float* qsrc = p.q_abs + qrow * kDc + 8 * g2;
-      const float* rsrc = p.q_rope + qrow * kDr + 8 * g2;
-      const float sc = head_ok ? p.scale_log2 : 0.f;
+      const vec* qsrc = reinterpret_cast<const vec*>(reinterpret_cast<const E*>(p.q_prep) + qrow * (kDc + kDr) + 8 * g2);
+      vec qr4[4];
 #pragma unroll
       for (int kk = 0; kk < 36; ++kk) {
-        const float* src = kk < 32 ? qsrc + 16 * kk : rsrc + 16 * (kk - 32);
-        const f32x4 a = *reinterpret_cast<const f32x4*>(src);
-        const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
-        vec v;
+        const vec v = qsrc[2 * kk];
+        if (kk < 32) qb[kk] = v;
+        else qr4[kk - 32] = v;
+      }
+      const vec zero = {};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[e] = (E)(a[e] * sc);
-          v[4 + e] = (E)(b[e] * sc);
-        }
+      for (int kk = 0; kk < 36; ++kk) {
         if (kk < 32) {
-          qb[kk] = v;
+          if (!head_ok) qb[kk] = zero;
         } else {
           const int j = 2 * (kk - 32) + g2;
-          lds_st(L, kQropeOff + head * 128 + ((j ^ (head & 7)) << 4), v);
+          lds_st(L, kQropeOff + head * 128 + ((j ^ fr(head)) << 4), head_ok ? qr4[kk - 32] : zero);
         }
-        __builtin_amdgcn_sched_barrier(0);  // bound the loads in flight (register pressure)
       }
     }
 
@@ -366,141 +491,175 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     rotate_rows<KT>(L, 0, wave, lane0);
     if (ntiles > 1) rotate_rows<KT>(L, kBufBytes, wave, lane0);
 
-    for (int t = 0; t < ntiles; ++t) {
-      lds_barrier();  // tile t staged and rotated by every wave; tile t-1 fully consumed
+    // Software pipeline over tiles; iteration t (from -1):
+    //   QK(t+1) -> s_next, with softmax(t) on s_cur interleaved between its
+    //   MFMAs and the HBM->LDS copies of tile t+2 riding along;
+    //   PV(t): O += P(t) . V(t); then RoPE of tile t+2 (own rows) and a barrier.
+    // Buffers: tile k lives in buffer k % 3. In iteration t, V(t) and K(t+1)
+    // are read and tile t+2 is written; t+2 = t-1 (mod 3) was last read in
+    // iteration t-1, before the barrier that opens iteration t.
+    // Every LDS read that a static lgkmcnt count includes is always issued;
+    // where its data is not needed it reads a valid buffer and is dropped.
+    f32x16 s_cur = {};
+    for (int t = -1; t < ntiles; ++t) {
+      lds_barrier();  // tile t+1 staged and rotated by every wave; iteration t-1 done
       const int lane = opaque(tid & 63);
       const int g2 = lane >> 5;
       const int q16 = lane >> 4, s16 = lane & 15;
       const int head = 32 * wave + (lane & 31);
-      if (t + 2 < ntiles) issue_tile_dma(p, sg, t + 2, L, ((t + 2) % kNBuf) * kBufBytes, wave, lane);
-      const uint32_t cur = (t % kNBuf) * kBufBytes;
+      const bool sm = t >= 0;                   // softmax(t) and PV(t)
+      const bool do_dma = sm && t + 2 < ntiles;  // tile t+2: copies and RoPE
+      const uint32_t cur = ((t < 0 ? 0 : t) % kNBuf) * kBufBytes;  // t = -1: tile 0, with P = 0
+      const uint32_t nxt = ((t + 1) % kNBuf) * kBufBytes;
+      const uint32_t dbuf = ((t + 2) % kNBuf) * kBufBytes;
 
-      // ---- S^T[pos][head] over 36 k-steps (32 latent + 4 rope) ----
-      // A operand of k-step kk: row arow, logical chunk 2kk + g2, stored at
-      // 2(kk ^ (af>>1)) + (g2 ^ (af&1)). For kk = 4m + r that is byte offset
-      // 128m + 32(r ^ (af>>1)) + 16(g2 ^ (af&1)). A operands are prefetched two
-      // k-steps ahead.
-      const int arow = lane & 31;
-      const int af = swzf(arow & 7);
-      const uint32_t ct_row = cur + arow * 1024 + 16 * (g2 ^ (af & 1));
-      const uint32_t rp_row = cur + kRopeOff + arow * 128 + 16 * (g2 ^ (af & 1));
-      auto a_off = [&](int kk) -> uint32_t {
-        const uint32_t o = 32 * ((kk & 3) ^ (af >> 1)) + 128 * (kk >> 2);
-        return kk < 32 ? ct_row + o : rp_row + o - 128 * 8;
-      };
-      const uint32_t qr_row = kQropeOff + head * 128;
-      // two independent accumulation chains (even / odd k-steps)
-      f32x16 s0, s1;
-      vec an0 = lds_ld<vec>(L, a_off(0)), an1 = lds_ld<vec>(L, a_off(1));
-#pragma unroll
-      for (int kk = 0; kk < 36; kk += 2) {
-        const vec a0 = an0, a1 = an1;
-        if (kk + 2 < 36) {
-          an0 = lds_ld<vec>(L, a_off(kk + 2));
-          an1 = lds_ld<vec>(L, a_off(kk + 3));
-        }
-        if (kk == 0) {
-          O_::mma_v0(s0, a0, qb[0]);
-          O_::mma_v0(s1, a1, qb[1]);
-        } else if (kk < 32) {
-          O_::mma_v(s0, a0, qb[kk]);
-          O_::mma_v(s1, a1, qb[kk + 1]);
-        } else {
-          const vec b0 = lds_ld<vec>(L, qr_row + (((2 * (kk - 32) + g2) ^ (head & 7)) << 4));
-          const vec b1 = lds_ld<vec>(L, qr_row + (((2 * (kk - 31) + g2) ^ (head & 7)) << 4));
-          O_::mma_v(s0, a0, b0);
-          O_::mma_v(s1, a1, b1);
-        }
-      }
-      settle(s0, s1);
-      f32x16 sc = s0 + s1;
-
-      // ---- lazy online softmax; lane = head, 16 positions 8(i/4)+4*g2+(i%4) ----
+      // ---- softmax(t) pieces, run between the QK(t+1) MFMAs ----
+      // s_cur lane = head, 16 positions 8(i/4) + 4*g2 + (i%4); lazy base-2
+      // online softmax: P = 2^(s - m) with m raised only when a score exceeds
+      // it by more than kRescaleSlack (then O and l are rescaled).
       const int valid = min(kT, seg_len - t * kT);
       float lmax = -INFINITY;
+      vec pv[2] = {};
+      auto sm_mask_max = [&]() {
+        settle1(s_cur);
+        if (valid < kT) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int pos = 8 * (i >> 2) + 4 * g2 + (i & 3);
-        sc[i] = pos < valid ? sc[i] : -INFINITY;
-        lmax = fmaxf(lmax, sc[i]);
-      }
-      const bool need = lmax > m_run + (float)kRescaleSlack;
-      if (__builtin_amdgcn_ballot_w64(need) != 0) {
-        const float tmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
-        const float m_new = fmaxf(m_run, tmax);
-        const bool first = m_run == -INFINITY;
-        const float alpha = first ? 0.f : exp2f(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
-        // O rows are heads 8(i/4) + 4*g2 + (i%4); alpha of head h sits in lane h.
-        if (__builtin_amdgcn_ballot_w64(!first && alpha != 1.f) != 0) {
-          if (lane < 32) lds_st(L, scratch + 4 * lane, alpha);
-          __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): own LDS write before own read
-          settle_acc(acc);
-          f32x16 a16;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const f32x4 a4 = lds_ld<f32x4>(L, scratch + 4 * (8 * q + 4 * g2));
-#pragma unroll
-            for (int r = 0; r < 4; ++r) a16[4 * q + r] = a4[r];
+          for (int i = 0; i < 16; ++i) {
+            const int pos = 8 * (i >> 2) + 4 * g2 + (i & 3);
+            s_cur[i] = pos < valid ? s_cur[i] : -INFINITY;
           }
-          // one 16-register block at a time, pinned back to AGPRs after each,
-          // so the rescale needs 16 temporaries instead of 256
-#pragma unroll
-          for (int nb = 0; nb < 16; ++nb) {
-            acc[nb] *= a16;
-            pin_agpr(acc[nb]);
-            __builtin_amdgcn_sched_barrier(0);
-          }
-          acc_ready(acc);
         }
-      }
-      vec pv[2];
+        float m4[4];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
+        for (int q = 0; q < 4; ++q)
+          m4[q] = fmaxf(fmaxf(s_cur[4 * q], s_cur[4 * q + 1]), fmaxf(s_cur[4 * q + 2], s_cur[4 * q + 3]));
+        lmax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+      };
+      auto sm_rescale = [&]() {
+        const bool need = lmax > m_run + (float)kRescaleSlack;
+        if (__builtin_amdgcn_ballot_w64(need) != 0) {
+          const float tmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
+          const float m_new = fmaxf(m_run, tmax);
+          const bool first = m_run == -INFINITY;
+          const float alpha = first ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+          m_run = m_new;
+          l_run *= alpha;
+          // O rows are heads 8(i/4) + 4*g2 + (i%4); alpha of head h sits in lane h.
+          if (__builtin_amdgcn_ballot_w64(!first && alpha != 1.f) != 0) {
+            if (lane < 32) lds_st(L, scratch + 4 * lane, alpha);
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): own LDS write before own read
+            settle_acc(acc);
+            f32x16 a16;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const f32x4 a4 = lds_ld<f32x4>(L, scratch + 4 * (8 * q + 4 * g2));
+#pragma unroll
+              for (int r = 0; r < 4; ++r) a16[4 * q + r] = a4[r];
+            }
+            // one 16-register block at a time, pinned back to AGPRs after each,
+            // so the rescale needs 16 temporaries instead of 256
+#pragma unroll
+            for (int nb = 0; nb < 16; ++nb) {
+              acc[nb] *= a16;
+              pin_agpr(acc[nb]);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+            acc_ready(acc);
+          }
+        }
+      };
+      // P = 2^(s - m) <= 2^kRescaleSlack; masked and far-below-max scores give 0
+      auto sm_exp = [&](int ks) {
+        float part[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const E pe = (E)exp2f(sc[8 * ks + j] - m_run);
+          const E pe = (E)__builtin_amdgcn_exp2f(s_cur[8 * ks + j] - m_run);
           pv[ks][j] = pe;
-          l_run += (float)pe;
+          part[j & 3] += (float)pe;
         }
-      }
+        l_run += (part[0] + part[1]) + (part[2] + part[3]);
+      };
+
+      // ---- QK(t+1): S^T[pos][head] over 36 k-steps (32 latent + 4 rope) ----
+      // A operand of k-step kk: tile row arow = lane%32, logical chunk
+      // 2kk + g2. For c_t (kk < 32) the byte offset inside the 1024-aligned row
+      // is 16((2kk + g2) ^ fc(arow)) = 32kk ^ 16(g2 ^ fc(arow)), so every
+      // address is one lane constant XOR an immediate; the same holds for the
+      // 128-B k_rope rows and the q_rope table with fr. A operands are read
+      // kQkDepth k-steps ahead of their MFMA. After the last tile the phase
+      // runs on a valid buffer and its result is dropped.
+      const int arow = lane & 31;
+      const uint32_t ct_x = (nxt + arow * 1024) | (16 * (g2 ^ fc(arow)));
+      const uint32_t rp_x = (nxt + kRopeOff + arow * 128) | (16 * (g2 ^ fr(arow)));
+      const uint32_t qr_x = (kQropeOff + head * 128) | (16 * (g2 ^ fr(head)));
+      auto a_off = [&](int kk) -> uint32_t { return kk < 32 ? (ct_x ^ (32 * kk)) : (rp_x ^ (32 * (kk - 32))); };
+
+      // PV(t) value reads: lane (q16, s16), read x of step (ks, nb) supplies
+      // the address of tile[rho][32nb + 16(q16&1) + 4(s16&3)], rho = 16ks + 8x
+      // + 4(q16>>1) + (s16>>2) (P's k-slot j of lane half g2 is position
+      // 16ks + 8(j>>2) + 4g2 + (j&3), the S^T accumulator layout). fc(rho) =
+      // 4(s16>>2) + 2x + (q16>>1) is independent of ks and nb, so the address
+      // is base_x ^ 64nb with 16384ks as the immediate offset.
+      const int lg = 2 * (q16 & 1) + ((s16 & 3) >> 1);
+      const uint32_t trow = cur + (4 * (q16 >> 1) + (s16 >> 2)) * 1024;
+      const uint32_t zlo = 64 * (s16 >> 2) + 8 * (s16 & 1);
+      const uint32_t tb0 = trow | (zlo + 16 * (lg ^ (q16 >> 1)));
+      const uint32_t tb1 = (trow + 8 * 1024) | (zlo + 16 * (lg ^ (2 + (q16 >> 1))));
+      TrPair tr[kPvDepth];
+      auto b_issue = [&](TrPair& r, auto step_c) {
+        constexpr int step = decltype(step_c)::value;
+        constexpr int ks = step >> 4, nb = step & 15;
+        r.x0 = lds_tr<16384 * ks>(L, tb0 ^ (64 * nb));
+        r.x1 = lds_tr<16384 * ks>(L, tb1 ^ (64 * nb));
+      };
+
+      f32x16 s_next;
+      vec ar[kQkDepth];
+      vec qr[4];
+      static_for<kQkDepth>([&](auto i) { ar[decltype(i)::value] = lds_rd128<vec>(L, a_off(decltype(i)::value)); });
+      static_for<36>([&](auto kk_c) {
+        constexpr int kk = decltype(kk_c)::value;
+        constexpr int D = kQkDepth;
+        if constexpr (kk == kQrAt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) qr[r] = lds_rd128<vec>(L, qr_x ^ (32 * r));
+        }
+        vec& a = ar[kk % D];
+        wait_lgkm<qk_later(kk)>(a);
+        if constexpr (kk < 32) {
+          if constexpr (kk == 0) O_::mma_v0(s_next, a, qb[kk]);
+          else O_::mma_v(s_next, a, qb[kk]);
+        } else {
+          O_::mma_v(s_next, a, qr[kk - 32]);
+        }
+        if constexpr (kk + D < 36) a = lds_rd128<vec>(L, a_off(kk + D));
+        if constexpr (kk % 3 == 2 && kk / 3 < kDmaPerWave) {
+          if (do_dma) issue_copy<kk / 3>(p, sg, t + 2, L, dbuf, wave, lane);
+        }
+        if constexpr (kk >= kTrAt && kk - kTrAt < kPvDepth) b_issue(tr[kk - kTrAt], std::integral_constant<int, kk - kTrAt>());
+        if constexpr (kk == kSmAt0) {
+          if (sm) sm_mask_max();
+        } else if constexpr (kk == kSmAt1) {
+          if (sm) sm_rescale();
+        } else if constexpr (kk == kSmAt2) {
+          if (sm) sm_exp(0);
+        } else if constexpr (kk == kSmAt3) {
+          if (sm) sm_exp(1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
       operands_ready(pv[0], pv[1]);
 
-      // ---- O[head][c] += P[head][pos] . tile[pos][c], 16 column blocks ----
-      // B operand for (ks, nb): rows 16ks + 8hf + 4(q16>>1) + (s16>>2) (row&7
-      // does not depend on ks, hf), logical chunk 4nb + jlo with
-      // jlo = 2(q16&1) + ((s16&3)>>1). With F = swzf(row), the physical chunk is
-      // 4(nb ^ (F>>2)) + (jlo ^ (F&3)): byte offset 64nb +- 64(F>>2) (sign by the
-      // parity of nb) + 16(jlo ^ (F&3)) -- two lane bases plus immediates.
-      const int trow = 4 * (q16 >> 1) + (s16 >> 2);
-      const int tf = swzf(trow);
-      const uint32_t tb = cur + trow * 1024 + 16 * ((2 * (q16 & 1) + ((s16 & 3) >> 1)) ^ (tf & 3)) + 8 * (s16 & 1);
-      const uint32_t tb_even = tb + 64 * (tf >> 2);
-      const uint32_t tb_odd = tb - 64 * (tf >> 2);
-      // The two transposed reads of step s+1 are issued before the MFMA of
-      // step s; lgkmcnt(2) then guarantees everything older than them (the
-      // reads of step s) has landed (LDS operations complete in order). The
-      // wait takes the raw read registers as operands so nothing copies them
-      // earlier.
-      auto b_issue = [&](int step) -> TrPair {
-        const int ks = step >> 4, nb = step & 15;
-        const uint32_t base = ((nb & 1) ? tb_odd : tb_even) + 64 * nb;
-        TrPair r;
-        r.x0 = lds_tr(L, base + (16 * ks) * 1024);
-        r.x1 = lds_tr(L, base + (16 * ks + 8) * 1024);
-        return r;
-      };
-      TrPair bn = b_issue(0);
-#pragma unroll
-      for (int step = 0; step < 32; ++step) {
-        TrPair bc = bn;
-        if (step + 1 < 32) {
-          bn = b_issue(step + 1);
-          asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(bc.x0), "+v"(bc.x1));
-        } else {
-          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(bc.x0), "+v"(bc.x1));
-        }
+      // ---- PV(t): O[head][c] += P[head][pos] . V[pos][c], 16 column blocks ----
+      // Step s waits for its value reads (count from pv_later: LDS operations
+      // complete in order), runs its MFMA, then issues the reads of step
+      // s + kPvDepth into the freed ring slot. After step kRotStep the four
+      // RoPE reads of tile t+2 go out (always; dropped without a tile).
+      RotIn rot;
+      static_for<32>([&](auto step_c) {
+        constexpr int step = decltype(step_c)::value;
+        TrPair& bc = tr[step % kPvDepth];
+        wait_lgkm<pv_later(step)>(bc.x0, bc.x1);
         i16x8 bv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -508,13 +667,16 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           bv[4 + e] = bc.x1[e];
         }
         O_::mma_a(acc[step & 15], pv[step >> 4], __builtin_bit_cast(vec, bv));
-      }
-
-      if (t + 1 < ntiles && t >= 1) {
-        if (t + 2 < ntiles) wait_vm<kDmaPerWave>();
-        else wait_vm<0>();
-        rotate_rows<KT>(L, ((t + 1) % kNBuf) * kBufBytes, wave, lane);
-      }
+        if constexpr (step + kPvDepth < 32) b_issue(bc, std::integral_constant<int, step + kPvDepth>());
+        if constexpr (step == kRotStep) {
+          wait_vm<0>();  // this wave's copies of tile t+2 have landed
+          rot = rot_issue(L, dbuf, wave, lane);
+        }
+      });
+      if (do_dma) rot_finish<KT>(L, rot);
+      else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(rot.ka), "+v"(rot.kb), "+v"(rot.c), "+v"(rot.s));
+      settle1(s_next);  // no VALU copy of s_next before the QK MFMAs have written it
+      s_cur = s_next;
     }
 
     // ---- segment end: l over both lane halves; normalise; write the slot ----
@@ -551,6 +713,31 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     lo = seg_hi;
     ++s;
   }
+}
+
+// q_prep[row] = E([q_abs[row] (dc) | q_rope[row] (dR)] * scale_log2); one
+// thread per 8 consecutive elements (72 per row for dc = 512, dR = 64).
+template <typename KT>
+__global__ __launch_bounds__(256) void prep_q_kernel(const float* __restrict__ q_abs, const float* __restrict__ q_rope,
+                                                     float scale, typename Ops<KT>::vec* __restrict__ out,
+                                                     int64_t rows) {
+  typedef typename Ops<KT>::elem E;
+  typedef typename Ops<KT>::vec vec;
+  constexpr int kPer = (kDc + kDr) / 8;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * kPer) return;
+  const int64_t row = i / kPer;
+  const int j = (int)(i - row * kPer);
+  const float* src = j < kDc / 8 ? q_abs + row * kDc + 8 * j : q_rope + row * kDr + 8 * (j - kDc / 8);
+  const f32x4 a = *reinterpret_cast<const f32x4*>(src);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
+  vec v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = (E)(a[e] * scale);
+    v[4 + e] = (E)(b[e] * scale);
+  }
+  out[i] = v;
 }
 
 template <typename KT>
@@ -598,6 +785,20 @@ bool mfma_supported(const DecodeProblem& p) {
       (reinterpret_cast<uintptr_t>(p.q_abs) & 15))
     return false;
   return device_is_gfx950();
+}
+
+hipError_t launch_prep_q(const DecodeProblem& p, hipStream_t stream) {
+  const int64_t rows = (int64_t)p.num_seqs * p.Hq;
+  const int64_t threads = rows * ((kDc + kDr) / 8);
+  if (threads == 0) return hipSuccess;
+  const unsigned blocks = (unsigned)((threads + 255) / 256);
+  if (p.kv_dtype == LA_DTYPE_BF16)
+    hipLaunchKernelGGL(prep_q_kernel<__hip_bfloat16>, dim3(blocks), dim3(256), 0, stream, p.q_abs, p.q_rope,
+                       p.scale_log2, reinterpret_cast<Ops<__hip_bfloat16>::vec*>(p.q_prep), rows);
+  else
+    hipLaunchKernelGGL(prep_q_kernel<__half>, dim3(blocks), dim3(256), 0, stream, p.q_abs, p.q_rope, p.scale_log2,
+                       reinterpret_cast<Ops<__half>::vec*>(p.q_prep), rows);
+  return hipGetLastError();
 }
 
 hipError_t launch_decode_mfma(const DecodeProblem& p, hipStream_t stream) {
