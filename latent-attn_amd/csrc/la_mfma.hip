@@ -70,7 +70,8 @@ constexpr int kPvDepth = 7;            // value reads this many PV steps ahead (
 constexpr int kRotStep = 27;           // PV step after which the RoPE reads of tile t+2 are issued
 constexpr int kQrAt = 32 - kQkDepth;   // QK step before which the q_rope table reads are issued
 constexpr int kTrAt = 36 - kPvDepth;   // QK steps kTrAt.. issue the first kPvDepth PV value-read pairs
-constexpr int kSmAt0 = 1, kSmAt1 = 4, kSmAt2 = 8, kSmAt3 = 14;  // softmax pieces after these QK steps
+constexpr int kSmSettle = 1;           // PV step after which softmax(t+1) starts (settle + mask)
+constexpr int kSmExp0 = 8;             // PV steps kSmExp0 .. +15 take one exp2 each
 
 // LDS issue order of one iteration (all reads counted by lgkmcnt):
 //   QK:  A(0..D-1); per step kk: [kk == kQrAt: 4 q_rope reads] wait A(kk),
@@ -445,8 +446,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
 
     lds_barrier();  // all waves are done with the previous segment's buffers
 
-    issue_tile_dma(p, sg, 0, L, 0, wave, lane0);
-    if (ntiles > 1) issue_tile_dma(p, sg, 1, L, kBufBytes, wave, lane0);
+    issue_tile_dma(p, sg, 0, L, 0, wave, lane0);  // tile 1 rides along iteration -1
 
     // Q^T as the B operand: lane holds Q[head][16kk + 8*g2 .. +8], pre-scaled.
     // The 32 latent k-steps stay in VGPRs; the 4 rope k-steps go to this
@@ -489,96 +489,56 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
 
     wait_vm<0>();
     rotate_rows<KT>(L, 0, wave, lane0);
-    if (ntiles > 1) rotate_rows<KT>(L, kBufBytes, wave, lane0);
 
     // Software pipeline over tiles; iteration t (from -1):
-    //   QK(t+1) -> s_next, with softmax(t) on s_cur interleaved between its
-    //   MFMAs and the HBM->LDS copies of tile t+2 riding along;
-    //   PV(t): O += P(t) . V(t); then RoPE of tile t+2 (own rows) and a barrier.
+    //   [apply the O rescale decided by softmax(t)]
+    //   QK(t+1) -> s_next, with the HBM->LDS copies of tile t+2 riding along;
+    //   PV(t): O += P(t) . V(t), with softmax(t+1) (s_next -> P(t+1)) spread
+    //   between its MFMAs; then RoPE of tile t+2 (own rows) and a barrier.
     // Buffers: tile k lives in buffer k % 3. In iteration t, V(t) and K(t+1)
     // are read and tile t+2 is written; t+2 = t-1 (mod 3) was last read in
     // iteration t-1, before the barrier that opens iteration t.
     // Every LDS read that a static lgkmcnt count includes is always issued;
     // where its data is not needed it reads a valid buffer and is dropped.
-    f32x16 s_cur = {};
+    vec p_cur[2] = {};         // P(t); zero for t = -1
+    float alpha_pend = 1.f;    // O rescale owed before PV(t) (per head = lane % 32)
+    bool resc_pend = false;    // wave-uniform
     for (int t = -1; t < ntiles; ++t) {
       lds_barrier();  // tile t+1 staged and rotated by every wave; iteration t-1 done
       const int lane = opaque(tid & 63);
       const int g2 = lane >> 5;
       const int q16 = lane >> 4, s16 = lane & 15;
       const int head = 32 * wave + (lane & 31);
-      const bool sm = t >= 0;                   // softmax(t) and PV(t)
-      const bool do_dma = sm && t + 2 < ntiles;  // tile t+2: copies and RoPE
+      const bool sm = t + 1 < ntiles;  // softmax(t+1) runs in this iteration
+      const bool do_dma = t + 2 < ntiles;  // tile t+2: copies and RoPE
       const uint32_t cur = ((t < 0 ? 0 : t) % kNBuf) * kBufBytes;  // t = -1: tile 0, with P = 0
       const uint32_t nxt = ((t + 1) % kNBuf) * kBufBytes;
       const uint32_t dbuf = ((t + 2) % kNBuf) * kBufBytes;
 
-      // ---- softmax(t) pieces, run between the QK(t+1) MFMAs ----
-      // s_cur lane = head, 16 positions 8(i/4) + 4*g2 + (i%4); lazy base-2
-      // online softmax: P = 2^(s - m) with m raised only when a score exceeds
-      // it by more than kRescaleSlack (then O and l are rescaled).
-      const int valid = min(kT, seg_len - t * kT);
-      float lmax = -INFINITY;
-      vec pv[2] = {};
-      auto sm_mask_max = [&]() {
-        settle1(s_cur);
-        if (valid < kT) {
+      // ---- O *= alpha for heads whose running max moved in softmax(t) ----
+      // O rows are heads 8(i/4) + 4*g2 + (i%4); alpha of head h sits in lane h.
+      if (resc_pend) {
+        if (lane < 32) lds_st(L, scratch + 4 * lane, alpha_pend);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): own LDS write before own read
+        settle_acc(acc);
+        f32x16 a16;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int pos = 8 * (i >> 2) + 4 * g2 + (i & 3);
-            s_cur[i] = pos < valid ? s_cur[i] : -INFINITY;
-          }
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 a4 = lds_ld<f32x4>(L, scratch + 4 * (8 * q + 4 * g2));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) a16[4 * q + r] = a4[r];
         }
-        float m4[4];
+        // one 16-register block at a time, pinned back to AGPRs after each,
+        // so the rescale needs 16 temporaries instead of 256
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          m4[q] = fmaxf(fmaxf(s_cur[4 * q], s_cur[4 * q + 1]), fmaxf(s_cur[4 * q + 2], s_cur[4 * q + 3]));
-        lmax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
-      };
-      auto sm_rescale = [&]() {
-        const bool need = lmax > m_run + (float)kRescaleSlack;
-        if (__builtin_amdgcn_ballot_w64(need) != 0) {
-          const float tmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
-          const float m_new = fmaxf(m_run, tmax);
-          const bool first = m_run == -INFINITY;
-          const float alpha = first ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-          m_run = m_new;
-          l_run *= alpha;
-          // O rows are heads 8(i/4) + 4*g2 + (i%4); alpha of head h sits in lane h.
-          if (__builtin_amdgcn_ballot_w64(!first && alpha != 1.f) != 0) {
-            if (lane < 32) lds_st(L, scratch + 4 * lane, alpha);
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): own LDS write before own read
-            settle_acc(acc);
-            f32x16 a16;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const f32x4 a4 = lds_ld<f32x4>(L, scratch + 4 * (8 * q + 4 * g2));
-#pragma unroll
-              for (int r = 0; r < 4; ++r) a16[4 * q + r] = a4[r];
-            }
-            // one 16-register block at a time, pinned back to AGPRs after each,
-            // so the rescale needs 16 temporaries instead of 256
-#pragma unroll
-            for (int nb = 0; nb < 16; ++nb) {
-              acc[nb] *= a16;
-              pin_agpr(acc[nb]);
-              __builtin_amdgcn_sched_barrier(0);
-            }
-            acc_ready(acc);
-          }
+        for (int nb = 0; nb < 16; ++nb) {
+          acc[nb] *= a16;
+          pin_agpr(acc[nb]);
+          __builtin_amdgcn_sched_barrier(0);
         }
-      };
-      // P = 2^(s - m) <= 2^kRescaleSlack; masked and far-below-max scores give 0
-      auto sm_exp = [&](int ks) {
-        float part[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const E pe = (E)__builtin_amdgcn_exp2f(s_cur[8 * ks + j] - m_run);
-          pv[ks][j] = pe;
-          part[j & 3] += (float)pe;
-        }
-        l_run += (part[0] + part[1]) + (part[2] + part[3]);
-      };
+        acc_ready(acc);
+        resc_pend = false;
+      }
 
       // ---- QK(t+1): S^T[pos][head] over 36 k-steps (32 latent + 4 rope) ----
       // A operand of k-step kk: tile row arow = lane%32, logical chunk
@@ -637,24 +597,64 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           if (do_dma) issue_copy<kk / 3>(p, sg, t + 2, L, dbuf, wave, lane);
         }
         if constexpr (kk >= kTrAt && kk - kTrAt < kPvDepth) b_issue(tr[kk - kTrAt], std::integral_constant<int, kk - kTrAt>());
-        if constexpr (kk == kSmAt0) {
-          if (sm) sm_mask_max();
-        } else if constexpr (kk == kSmAt1) {
-          if (sm) sm_rescale();
-        } else if constexpr (kk == kSmAt2) {
-          if (sm) sm_exp(0);
-        } else if constexpr (kk == kSmAt3) {
-          if (sm) sm_exp(1);
-        }
         __builtin_amdgcn_sched_barrier(0);
       });
-      operands_ready(pv[0], pv[1]);
+
+      // ---- softmax(t+1) pieces, spread over the PV(t) steps ----
+      // s_next lane = head, 16 positions 8(i/4) + 4*g2 + (i%4); lazy base-2
+      // online softmax: P = 2^(s - m) with m raised only when a score exceeds
+      // it by more than kRescaleSlack; O's matching rescale is applied at the
+      // top of the next iteration, after PV(t) has added P(t) . V(t) at the
+      // old scale.
+      const int valid = min(kT, seg_len - (t + 1) * kT);
+      float m4[4];
+      float lmax = -INFINITY;
+      vec p_next[2] = {};
+      float lpart[4] = {0.f, 0.f, 0.f, 0.f};
+      auto sm_piece = [&](auto step_c) {
+        constexpr int step = decltype(step_c)::value;
+        if constexpr (step == kSmSettle) {
+          settle1(s_next);
+          if (sm && valid < kT) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int pos = 8 * (i >> 2) + 4 * g2 + (i & 3);
+              s_next[i] = pos < valid ? s_next[i] : -INFINITY;
+            }
+          }
+        } else if constexpr (step >= kSmSettle + 1 && step <= kSmSettle + 4) {
+          constexpr int q = step - kSmSettle - 1;
+          m4[q] = fmaxf(fmaxf(s_next[4 * q], s_next[4 * q + 1]), fmaxf(s_next[4 * q + 2], s_next[4 * q + 3]));
+        } else if constexpr (step == kSmSettle + 5) {
+          lmax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+          const bool need = sm && lmax > m_run + (float)kRescaleSlack;
+          if (__builtin_amdgcn_ballot_w64(need) != 0) {
+            const float tmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
+            const float m_new = fmaxf(m_run, tmax);
+            const bool first = m_run == -INFINITY;
+            const float alpha = first ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
+            alpha_pend = alpha;
+            resc_pend = __builtin_amdgcn_ballot_w64(!first && alpha != 1.f) != 0;
+          }
+        } else if constexpr (step >= kSmExp0 && step < kSmExp0 + 16) {
+          // P = 2^(s - m) <= 2^kRescaleSlack; masked and far-below-max scores give 0
+          constexpr int i = step - kSmExp0;
+          const E pe = (E)__builtin_amdgcn_exp2f(s_next[i] - m_run);
+          p_next[i >> 3][i & 7] = pe;
+          lpart[i & 3] += (float)pe;
+        } else if constexpr (step == kSmExp0 + 16) {
+          if (sm) l_run += (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
+        }
+      };
 
       // ---- PV(t): O[head][c] += P[head][pos] . V[pos][c], 16 column blocks ----
       // Step s waits for its value reads (count from pv_later: LDS operations
       // complete in order), runs its MFMA, then issues the reads of step
       // s + kPvDepth into the freed ring slot. After step kRotStep the four
       // RoPE reads of tile t+2 go out (always; dropped without a tile).
+      operands_ready(p_cur[0], p_cur[1]);
       RotIn rot;
       static_for<32>([&](auto step_c) {
         constexpr int step = decltype(step_c)::value;
@@ -666,17 +666,19 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           bv[e] = bc.x0[e];
           bv[4 + e] = bc.x1[e];
         }
-        O_::mma_a(acc[step & 15], pv[step >> 4], __builtin_bit_cast(vec, bv));
+        O_::mma_a(acc[step & 15], p_cur[step >> 4], __builtin_bit_cast(vec, bv));
         if constexpr (step + kPvDepth < 32) b_issue(bc, std::integral_constant<int, step + kPvDepth>());
         if constexpr (step == kRotStep) {
           wait_vm<0>();  // this wave's copies of tile t+2 have landed
           rot = rot_issue(L, dbuf, wave, lane);
         }
+        sm_piece(step_c);
+        __builtin_amdgcn_sched_barrier(0);
       });
       if (do_dma) rot_finish<KT>(L, rot);
       else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(rot.ka), "+v"(rot.kb), "+v"(rot.c), "+v"(rot.s));
-      settle1(s_next);  // no VALU copy of s_next before the QK MFMAs have written it
-      s_cur = s_next;
+      p_cur[0] = p_next[0];
+      p_cur[1] = p_next[1];
     }
 
     // ---- segment end: l over both lane halves; normalise; write the slot ----
