@@ -131,6 +131,18 @@ def decode_args(inp, out, capi):
     return a
 
 
+def measured_traffic(config: str):
+    """HBM bytes per attention-kernel launch measured with rocprofv3
+    (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size), read from the
+    committed profile summary for this workload; None if there is none."""
+    path = os.path.join(ROOT, "profiles", f"decode_mfma_{config}_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(inp, budget_s: float = 12.0):
     """Time the oracle's absorbed float32 path (this repo's CPU restatement of
     the reference math) on whole sequences of the workload, one at a time,
@@ -187,6 +199,9 @@ def main():
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--variant", type=int, default=0, help="0 auto, 1 VALU kernel, 2 MFMA kernel")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run 3 device-to-device copies of MIB MiB (the known-size kernel that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE into bytes) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs on a single MI355X "
@@ -198,6 +213,15 @@ def main():
     from latent_attn import capi
 
     device = torch.device("cuda:0")
+    if args.calibrate_copy > 0:
+        n = args.calibrate_copy << 20
+        src = torch.ones(n, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_read": n, "bytes_written": n, "launches": 3}), flush=True)
+        return
     lib = capi.load()
     hip = hip_runtime()
     log(f"[bench] building inputs for {args.config}")
@@ -284,7 +308,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.config),
         },
     }
     for b, e in evs:

@@ -210,16 +210,17 @@ int run(const la_decode_args* a, hipStream_t stream) {
       if (e != hipSuccess) return finish(e);
     }
     // the optional events bracket the attention kernel alone
-    if (a->decode_event_begin) {
-      hipError_t e = hipEventRecord(static_cast<hipEvent_t>(a->decode_event_begin), stream);
-      if (e != hipSuccess) return finish(e);
+    hipEvent_t ev_b = static_cast<hipEvent_t>(a->decode_event_begin);
+    hipEvent_t ev_e = static_cast<hipEvent_t>(a->decode_event_end);
+    hipError_t e = hipSuccess;
+    if (plan.mfma) {
+      e = launch_decode_mfma(p, stream, ev_b, ev_e);  // recorded by the launch itself
+    } else {
+      if (ev_b) e = hipEventRecord(ev_b, stream);
+      if (e == hipSuccess) e = launch_decode_generic(p, stream);
+      if (e == hipSuccess && ev_e) e = hipEventRecord(ev_e, stream);
     }
-    hipError_t e = plan.mfma ? launch_decode_mfma(p, stream) : launch_decode_generic(p, stream);
     if (e != hipSuccess) return finish(e);
-    if (a->decode_event_end) {
-      e = hipEventRecord(static_cast<hipEvent_t>(a->decode_event_end), stream);
-      if (e != hipSuccess) return finish(e);
-    }
   }
   return finish(project_mfma_supported(p) ? launch_combine_project_mfma(p, stream)
                                            : launch_combine_project(p, stream));

@@ -120,7 +120,9 @@ hipError_t launch_decode_generic(const DecodeProblem& p, hipStream_t stream);
 bool generic_supported(const DecodeProblem& p);
 
 // MFMA split-KV decode for 16-bit caches with kv_lora_rank 512, qk_rope_head_dim 64.
-hipError_t launch_decode_mfma(const DecodeProblem& p, hipStream_t stream);
+// ev_begin / ev_end (optional) are recorded at the kernel's start and end.
+hipError_t launch_decode_mfma(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_begin = nullptr,
+                              hipEvent_t ev_end = nullptr);
 bool mfma_supported(const DecodeProblem& p);
 int mfma_heads_per_group();
 int mfma_max_chunk_rows();

@@ -41,6 +41,8 @@
 //     partial slot (chunk + sequence); la_proj.hip merges the slots.
 #include "la_internal.hpp"
 
+#include <hip/hip_ext.h>
+
 #include <cstring>
 #include <mutex>
 #include <type_traits>
@@ -743,7 +745,7 @@ __global__ __launch_bounds__(256) void prep_q_kernel(const float* __restrict__ q
 }
 
 template <typename KT>
-hipError_t launch_t(const DecodeProblem& p, hipStream_t stream) {
+hipError_t launch_t(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
   static bool attr_set = false;  // per instance; setting it twice is harmless
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_mfma_kernel<KT>),
@@ -753,7 +755,14 @@ hipError_t launch_t(const DecodeProblem& p, hipStream_t stream) {
   }
   const int groups = (p.Hq + kHG - 1) / kHG;
   const int64_t blocks = groups == 1 ? p.num_chunks : (int64_t)((p.num_chunks + 7) / 8) * 8 * groups;
-  hipLaunchKernelGGL((decode_mfma_kernel<KT>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, stream, p, groups);
+  if (ev_begin || ev_end) {
+    // the events time this kernel's execution alone (no dispatch gap)
+    hipExtLaunchKernelGGL((decode_mfma_kernel<KT>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, stream,
+                          ev_begin, ev_end, 0, p, groups);
+  } else {
+    hipLaunchKernelGGL((decode_mfma_kernel<KT>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, stream, p,
+                       groups);
+  }
   return hipGetLastError();
 }
 
@@ -803,9 +812,9 @@ hipError_t launch_prep_q(const DecodeProblem& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_decode_mfma(const DecodeProblem& p, hipStream_t stream) {
-  if (p.kv_dtype == LA_DTYPE_BF16) return launch_t<__hip_bfloat16>(p, stream);
-  return launch_t<__half>(p, stream);
+hipError_t launch_decode_mfma(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
+  if (p.kv_dtype == LA_DTYPE_BF16) return launch_t<__hip_bfloat16>(p, stream, ev_begin, ev_end);
+  return launch_t<__half>(p, stream, ev_begin, ev_end);
 }
 
 }  // namespace la

@@ -149,3 +149,37 @@ def test_functional_signatures_match_reference():
     assert MLAConfig.deepseek_v2() == MLAConfig(5120, 512, 128, 64, 128, 128)
     assert MLAConfig.deepseek_v3() == MLAConfig(7168, 512, 128, 64, 128, 128)
     assert MLAConfig.deepseek_v2().bytes_per_kv_entry() == 1152
+
+
+def test_cpp_dropin_header_compiles_and_links(tmp_path):
+    """include/latent_attn.hpp: reference-style aggregate initialisation of
+    FusedMLAParams / BatchedFusedMLAParams (src/fused_mla.cuh:11-34,
+    src/fused_mla_batched.cuh:7-30) compiles with HIP types and links against
+    the library; the workspace query runs on the host."""
+    import os
+    import shutil
+    import subprocess
+
+    REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    gxx = shutil.which("g++")
+    if gxx is None or not os.path.isdir("/opt/rocm/include/hip"):
+        pytest.skip("g++ or HIP headers not available")
+    src = tmp_path / "dropin.cpp"
+    src.write_text(
+        '#include "latent_attn.hpp"\n'
+        "int main() {\n"
+        "  latent_attn::MLAConfig cfg = latent_attn::MLAConfig::deepseek_v2();\n"
+        "  cfg.validate();\n"
+        "  latent_attn::FusedMLAParams p{nullptr, 16, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, &cfg};\n"
+        "  latent_attn::BatchedFusedMLAParams b{nullptr, 16, 2, nullptr, nullptr, nullptr, nullptr, nullptr,\n"
+        "                                      nullptr, &cfg};\n"
+        "  if (p.kv_dtype != LA_DTYPE_F16 || b.batch_size != 2) return 2;\n"
+        "  if (latent_attn::launch_fused_mla(latent_attn::FusedMLAParams{}) != hipErrorInvalidValue) return 3;\n"
+        "  return latent_attn::fused_mla_workspace_size(16, 2, cfg) > 0 ? 0 : 1;\n"
+        "}\n")
+    libdir = os.path.join(REPO, "latent-attn_amd", "latent_attn")
+    exe = tmp_path / "dropin"
+    subprocess.run([gxx, "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                    "-I" + os.path.join(REPO, "include"), str(src), "-o", str(exe), "-L" + libdir,
+                    "-llatent_attn_hip", "-Wl,-rpath," + libdir], check=True)
+    assert subprocess.run([str(exe)]).returncode == 0
