@@ -55,7 +55,8 @@ struct Plan {
   int chunk_len = 0;
   int num_chunks = 0;
   int num_slots = 0;
-  size_t q_abs_off = 0, q_prep_off = 0, part_o_off = 0, part_lse_off = 0, total = 0;
+  bool proj_mfma = false;
+  size_t q_abs_off = 0, q_prep_off = 0, part_o_off = 0, part_lse_off = 0, o_merged_off = 0, total = 0;
 };
 
 // Fills the problem (without workspace pointers) and the plan. The args'
@@ -150,6 +151,11 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   off += align_up((size_t)pl.num_slots * p->Hq * c.kv_lora_rank * sizeof(float));
   pl.part_lse_off = off;
   off += align_up((size_t)pl.num_slots * p->Hq * sizeof(float));
+  pl.proj_mfma = project_mfma_supported(*p);
+  if (pl.proj_mfma) {
+    pl.o_merged_off = off;
+    off += align_up(combine_project_mfma_workspace(*p));
+  }
   pl.total = off;
 
   p->chunk_len = pl.chunk_len;
@@ -222,8 +228,9 @@ int run(const la_decode_args* a, hipStream_t stream) {
     }
     if (e != hipSuccess) return finish(e);
   }
-  return finish(project_mfma_supported(p) ? launch_combine_project_mfma(p, stream)
-                                           : launch_combine_project(p, stream));
+  return finish(plan.proj_mfma
+                    ? launch_combine_project_mfma(p, reinterpret_cast<float*>(ws + plan.o_merged_off), stream)
+                    : launch_combine_project(p, stream));
 }
 
 la_decode_args shared_cache_args(const void* kv_cache, int kv_dtype, int seq_len, int batch, const float* q_absorbed,

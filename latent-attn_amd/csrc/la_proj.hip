@@ -18,11 +18,13 @@
 //          block] (128 x 128) is staged in LDS; wave w owns 32 columns; the
 //          B operand (8 consecutive rows i per lane) comes from
 //          ds_read_b64_tr_b16.
-// project: grid (nh, ceil(R/32)), 256 threads. Phase 1 merges the partial
-//          slots of 32 query tokens of weight head h into LDS (hi/lo 16-bit);
-//          phase 2: wave w owns 32 output columns j, B operand = 16 contiguous
-//          bytes of a W_UV row read straight from global memory (each weight
-//          element is read once per block).
+// combine: merge_slots_kernel, one wave per (query row, weight head), writes
+//          the log-sum-exp merge of the partial slots (fp32, workspace).
+// project: grid (nh, ceil(R/32)), 256 threads. Phase 1 stages the merged O of
+//          32 query tokens of weight head h in LDS (hi/lo 16-bit); phase 2:
+//          wave w owns 32 output columns j, B operand = 16 contiguous bytes of
+//          a W_UV row read straight from global memory (each weight element is
+//          read once per block).
 #include "la_internal.hpp"
 
 namespace la {
@@ -149,11 +151,73 @@ constexpr int kDcP = 512;
 constexpr int kORowBytes = kDcP * 2 + 16;  // 16-bit O row + pad (8 rows -> 8 bank groups)
 constexpr int kProjLdsBytes = 2 * 32 * kORowBytes;
 
+// merge: one wave per (query row r, weight head h). o_merged[r][h][:] =
+// sum_slots 2^(lse_s - m) * part_o_s / sum_slots 2^(lse_s - m), m = max lse
+// (reference has no split; the merge is exact in real arithmetic). Lane l owns
+// latent columns 8l .. 8l+7; the slot loads go out 8 at a time.
+constexpr int kMergeWaves = 4;
+
+__global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodeProblem p, float* __restrict__ o_merged) {
+  const int lane = threadIdx.x & 63;
+  const int64_t pair = (int64_t)blockIdx.x * kMergeWaves + (threadIdx.x >> 6);
+  const int R = p.num_seqs * p.qps;
+  if (pair >= (int64_t)R * p.nh) return;
+  const int r = (int)(pair / p.nh), h = (int)(pair % p.nh);
+  const int s = r / p.qps;
+  const int hq = (r % p.qps) * p.nh + h;
+  f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
+  const int64_t lo = seq_begin(p, s), hi = seq_begin(p, s + 1);
+  if (hi > lo) {
+    const int64_t cf = lo / p.chunk_len;
+    const int n = (int)((hi - 1) / p.chunk_len - cf + 1);  // slots cf+s .. cf+s+n-1
+    const float* lse = p.part_lse + (cf + s) * p.Hq + hq;
+    const float* src = p.part_o + ((cf + s) * p.Hq + hq) * kDcP + 8 * lane;
+    const int64_t sstride = (int64_t)p.Hq * kDcP;
+    float mx = -INFINITY;
+    for (int i = lane; i < n; i += 64) mx = fmaxf(mx, lse[(int64_t)i * p.Hq]);
+    mx = wave_max(mx);
+    float wsum = 0.f;
+    for (int i0 = 0; i0 < n; i0 += 64) {
+      const int nb = min(64, n - i0);
+      const float wl = lane < nb ? exp2f(lse[(int64_t)(i0 + lane) * p.Hq] - mx) : 0.f;
+      wsum += wave_sum(wl);
+      for (int j = 0; j < nb; j += 8) {
+        f32x4 d0[8], d1[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (j + u < nb) {
+            const float* q = src + (int64_t)(i0 + j + u) * sstride;
+            d0[u] = *reinterpret_cast<const f32x4*>(q);
+            d1[u] = *reinterpret_cast<const f32x4*>(q + 4);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (j + u < nb) {
+            const float w = __shfl(wl, j + u, 64);
+            o0 += w * d0[u];
+            o1 += w * d1[u];
+          }
+        }
+      }
+    }
+    const float inv = 1.f / wsum;
+    o0 *= inv;
+    o1 *= inv;
+  }
+  float* dst = o_merged + ((int64_t)r * p.nh + h) * kDcP + 8 * lane;
+  *reinterpret_cast<f32x4*>(dst) = o0;
+  *reinterpret_cast<f32x4*>(dst + 4) = o1;
+}
+
+// project: grid (nh, ceil(R/32)), 256 threads. Phase 1 stages the merged O of
+// 32 query rows of weight head h into LDS (16-bit hi/lo); phase 2: wave w owns
+// 32 output columns j, B operand = 16 contiguous bytes of a W_UV row read
+// straight from global memory (each weight element is read once per block).
 template <typename WT>
-__global__ __launch_bounds__(256) void combine_project_mfma_kernel(DecodeProblem p) {
+__global__ __launch_bounds__(256) void project_mfma_kernel(DecodeProblem p, const float* __restrict__ o_merged) {
   typedef Mma<WT> M;
   typedef typename M::vec vec;
-  typedef typename M::elem E;
   extern __shared__ __attribute__((aligned(16))) char o_lds[];  // kProjLdsBytes
   char* o_hi = o_lds;
   char* o_lo = o_lds + 32 * kORowBytes;
@@ -161,38 +225,22 @@ __global__ __launch_bounds__(256) void combine_project_mfma_kernel(DecodeProblem
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int R = p.num_seqs * p.qps;
 
-  // ---- phase 1: merge the partial slots of 32 tokens into LDS ----
+  // ---- phase 1: merged O of 32 rows -> LDS (hi/lo) ----
   for (int rr = wave; rr < 32; rr += 4) {
     const int r = r0 + rr;
     float o[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = 0.f;
     if (r < R) {
-      const int s = r / p.qps;
-      const int hq = (r % p.qps) * p.nh + h;
-      const int64_t lo = seq_begin(p, s), hi = seq_begin(p, s + 1);
-      if (hi > lo) {
-        const int64_t cf = lo / p.chunk_len, cl = (hi - 1) / p.chunk_len;
-        float mx = -INFINITY;
-        for (int64_t c = cf; c <= cl; ++c) mx = fmaxf(mx, p.part_lse[(c + s) * p.Hq + hq]);
-        float wsum = 0.f;
-        for (int64_t c = cf; c <= cl; ++c) {
-          const int64_t slot = c + s;
-          const float w = exp2f(p.part_lse[slot * p.Hq + hq] - mx);
-          wsum += w;
-          const float* src = p.part_o + (slot * p.Hq + hq) * kDcP + lane * 8;
-          const f32x4 a = *reinterpret_cast<const f32x4*>(src);
-          const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
+      const float* src = o_merged + ((int64_t)r * p.nh + h) * kDcP + 8 * lane;
+      const f32x4 a = *reinterpret_cast<const f32x4*>(src);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            o[e] += w * a[e];
-            o[4 + e] += w * b[e];
-          }
-        }
-        const float inv = 1.f / wsum;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] *= inv;
+      for (int e = 0; e < 4; ++e) {
+        o[e] = a[e];
+        o[4 + e] = b[e];
       }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = 0.f;
     }
     vec vh, vl;
     split8<WT>(o, vh, vl);
@@ -248,23 +296,33 @@ bool project_mfma_supported(const DecodeProblem& p) {
 }
 
 template <typename WT>
-hipError_t launch_cp(const DecodeProblem& p, hipStream_t stream) {
+hipError_t launch_proj(const DecodeProblem& p, const float* o_merged, hipStream_t stream) {
   static bool attr_set = false;  // per instance; setting it twice is harmless
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&combine_project_mfma_kernel<WT>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&project_mfma_kernel<WT>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kProjLdsBytes);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   const int R = p.num_seqs * p.qps;
   dim3 grid(p.nh, (R + 31) / 32);
-  hipLaunchKernelGGL(combine_project_mfma_kernel<WT>, grid, dim3(256), kProjLdsBytes, stream, p);
+  hipLaunchKernelGGL(project_mfma_kernel<WT>, grid, dim3(256), kProjLdsBytes, stream, p, o_merged);
   return hipGetLastError();
 }
 
-hipError_t launch_combine_project_mfma(const DecodeProblem& p, hipStream_t stream) {
-  if (p.wuv_dtype == LA_DTYPE_BF16) return launch_cp<__hip_bfloat16>(p, stream);
-  return launch_cp<__half>(p, stream);
+size_t combine_project_mfma_workspace(const DecodeProblem& p) {
+  return (size_t)p.num_seqs * p.qps * p.nh * kDcP * sizeof(float);
+}
+
+hipError_t launch_combine_project_mfma(const DecodeProblem& p, float* o_merged, hipStream_t stream) {
+  const int64_t pairs = (int64_t)p.num_seqs * p.qps * p.nh;
+  if (pairs == 0) return hipSuccess;
+  hipLaunchKernelGGL(merge_slots_kernel, dim3((unsigned)((pairs + kMergeWaves - 1) / kMergeWaves)),
+                     dim3(kMergeWaves * 64), 0, stream, p, o_merged);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (p.wuv_dtype == LA_DTYPE_BF16) return launch_proj<__hip_bfloat16>(p, o_merged, stream);
+  return launch_proj<__half>(p, o_merged, stream);
 }
 
 }  // namespace la
