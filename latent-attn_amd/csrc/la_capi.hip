@@ -56,6 +56,8 @@ struct Plan {
   int num_chunks = 0;
   int num_slots = 0;
   bool proj_mfma = false;
+  bool absorb_mfma = false;  // q_nope . W_UK on the MFMA kernel
+  bool absorb_prep = false;  // ... writing the attention kernel's 16-bit Q rows directly
   size_t q_abs_off = 0, q_prep_off = 0, part_o_off = 0, part_lse_off = 0, o_merged_off = 0, total = 0;
 };
 
@@ -138,8 +140,12 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   pl.num_slots = nchunks > 0 ? (int)(nchunks + a->num_seqs - 1) : 0;
 
   const int64_t tokens = (int64_t)a->num_seqs * a->queries_per_seq;
+  pl.absorb_mfma = absorb && absorb_mfma_supported(a->w_uk_dtype, c.num_heads, c.qk_nope_head_dim, c.kv_lora_rank) &&
+                   (reinterpret_cast<uintptr_t>(a->q_nope) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(a->W_UK) & 15) == 0;
+  pl.absorb_prep = pl.mfma && pl.absorb_mfma;
   size_t off = 0;
-  if (absorb) {
+  if (absorb && !pl.absorb_prep) {
     pl.q_abs_off = off;
     off += align_up((size_t)tokens * c.num_heads * c.kv_lora_rank * sizeof(float));
   }
@@ -195,23 +201,28 @@ int run(const la_decode_args* a, hipStream_t stream) {
 
   const la_mla_config& c = a->cfg;
   const int64_t tokens = (int64_t)a->num_seqs * a->queries_per_seq;
+  if (plan.mfma) p.q_prep = ws + plan.q_prep_off;
   if (a->q_nope) {
-    float* qa = reinterpret_cast<float*>(ws + plan.q_abs_off);
-    hipError_t e =
-        absorb_mfma_supported(a->w_uk_dtype, c.num_heads, c.qk_nope_head_dim, c.kv_lora_rank) &&
-                (reinterpret_cast<uintptr_t>(a->q_nope) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->W_UK) & 15) == 0
-            ? launch_absorb_mfma(a->q_nope, a->W_UK, a->w_uk_dtype, qa, (int)tokens, c.num_heads,
-                                 c.qk_nope_head_dim, c.kv_lora_rank, stream)
-            : launch_absorb(a->q_nope, a->W_UK, a->w_uk_dtype, qa, (int)tokens, c.num_heads, c.qk_nope_head_dim,
-                            c.kv_lora_rank, stream);
+    hipError_t e = hipSuccess;
+    if (plan.absorb_prep) {
+      // absorbed, scaled 16-bit Q rows for the attention kernel in one pass
+      e = launch_absorb_mfma(a->q_nope, a->W_UK, a->w_uk_dtype, p.q_prep, p.kv_dtype == LA_DTYPE_BF16 ? 1 : 2,
+                             a->q_rope, p.scale_log2, c.qk_rope_head_dim, (int)tokens, c.num_heads,
+                             c.qk_nope_head_dim, c.kv_lora_rank, stream);
+    } else {
+      float* qa = reinterpret_cast<float*>(ws + plan.q_abs_off);
+      e = plan.absorb_mfma ? launch_absorb_mfma(a->q_nope, a->W_UK, a->w_uk_dtype, qa, 0, nullptr, 1.f, 0,
+                                                (int)tokens, c.num_heads, c.qk_nope_head_dim, c.kv_lora_rank, stream)
+                           : launch_absorb(a->q_nope, a->W_UK, a->w_uk_dtype, qa, (int)tokens, c.num_heads,
+                                           c.qk_nope_head_dim, c.kv_lora_rank, stream);
+      p.q_abs = qa;
+    }
     if (e != hipSuccess) return finish(e);
-    p.q_abs = qa;
   }
   p.part_o = reinterpret_cast<float*>(ws + plan.part_o_off);
   p.part_lse = reinterpret_cast<float*>(ws + plan.part_lse_off);
   if (plan.num_chunks > 0) {
-    if (plan.mfma) {
-      p.q_prep = ws + plan.q_prep_off;
+    if (plan.mfma && !plan.absorb_prep) {
       hipError_t e = launch_prep_q(p, stream);
       if (e != hipSuccess) return finish(e);
     }
@@ -335,8 +346,9 @@ int la_absorb_q(const float* q_nope, const void* W_UK, int w_uk_dtype, float* q_
   if (!q_nope || !W_UK || !q_absorbed) return LA_ERROR_INVALID_VALUE;
   const bool mfma = la::absorb_mfma_supported(w_uk_dtype, cfg->num_heads, cfg->qk_nope_head_dim, cfg->kv_lora_rank) &&
                     (reinterpret_cast<uintptr_t>(q_nope) & 15) == 0 && (reinterpret_cast<uintptr_t>(W_UK) & 15) == 0;
-  hipError_t e = mfma ? la::launch_absorb_mfma(q_nope, W_UK, w_uk_dtype, q_absorbed, tokens, cfg->num_heads,
-                                               cfg->qk_nope_head_dim, cfg->kv_lora_rank, static_cast<hipStream_t>(stream))
+  hipError_t e = mfma ? la::launch_absorb_mfma(q_nope, W_UK, w_uk_dtype, q_absorbed, 0, nullptr, 1.f, 0, tokens,
+                                               cfg->num_heads, cfg->qk_nope_head_dim, cfg->kv_lora_rank,
+                                               static_cast<hipStream_t>(stream))
                       : la::launch_absorb(q_nope, W_UK, w_uk_dtype, q_absorbed, tokens, cfg->num_heads,
                                           cfg->qk_nope_head_dim, cfg->kv_lora_rank, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? (int)LA_SUCCESS : la::record_hip(e);

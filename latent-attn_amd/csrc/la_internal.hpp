@@ -134,8 +134,11 @@ hipError_t launch_combine_project(const DecodeProblem& p, hipStream_t stream);
 
 // MFMA versions for 16-bit weights (la_proj.hip).
 bool absorb_mfma_supported(int w_dtype, int nh, int dn, int dc);
-hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype, float* q_abs, int tokens, int nh,
-                              int dn, int dc, hipStream_t stream);
+// out_mode 0: out = q_abs (fp32). 1 / 2: out = q_prep rows (bf16 / fp16) =
+// [q_abs | q_rope] * scale, as prep_q_kernel writes them.
+hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype, void* out, int out_mode,
+                              const float* q_rope, float scale, int dR, int tokens, int nh, int dn, int dc,
+                              hipStream_t stream);
 bool project_mfma_supported(const DecodeProblem& p);
 // Workspace bytes for the merged O (fp32, (num_seqs*Hq, dc)) the MFMA
 // combine + projection pair uses.

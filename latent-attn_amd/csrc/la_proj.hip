@@ -79,42 +79,63 @@ __device__ inline void split8(const float* x, typename Mma<WT>::vec& hi, typenam
 constexpr int kAbsCols = 128;            // columns per block
 constexpr int kAbsRowBytes = 256 + 32;   // 128 x 16-bit + pad: 4 tr rows hit 4 bank groups
 
-template <typename WT>
+// out_mode 0: q_abs (fp32, (T*nh, dc)). out_mode 1 / 2: q_prep rows (bf16 /
+// fp16, (T*nh, dc + dR)) = [q_abs | q_rope] * scale for the MFMA attention
+// kernel; blocks with cb == 0 also convert the q_rope part of their rows.
+// All global loads (q_nope for every k-step, the W_UK tile) are issued before
+// the first wait.
+// NKS = dn / 16 when known at compile time (8 for dn = 128: no guards, every
+// load unconditional), 0 for any dn <= 128 that is a multiple of 16.
+template <typename WT, int NKS>
 __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restrict__ q_nope, const WT* __restrict__ W,
-                                                          float* __restrict__ q_abs, int tokens, int nh, int dn,
-                                                          int dc) {
+                                                          void* __restrict__ out, int out_mode,
+                                                          const float* __restrict__ q_rope, float scale, int dR,
+                                                          int tokens, int nh, int dn, int dc) {
   typedef Mma<WT> M;
   typedef typename M::vec vec;
   __shared__ __attribute__((aligned(16))) char wt[128 * kAbsRowBytes];  // dn <= 128 rows
   const int h = blockIdx.x, cb = blockIdx.y, t0 = blockIdx.z * 32;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int nks = NKS > 0 ? NKS : dn / 16;  // <= 8
+  if (NKS > 0) dn = 16 * NKS;
 
-  // stage W_UK[h*dn + i][cb*128 + 0..127] for i < dn (16 B per thread-load)
-  for (int q = tid; q < dn * 16; q += 256) {
-    const int i = q >> 4, ch = q & 15;
-    const i16x8 v = *reinterpret_cast<const i16x8*>(W + ((int64_t)h * dn + i) * dc + cb * kAbsCols + ch * 8);
-    *reinterpret_cast<i16x8*>(wt + i * kAbsRowBytes + ch * 16) = v;
+  // q_nope of token t0 + lane%32, elements 16ks + 8(lane/32) .. +8, all k-steps
+  const int t = t0 + (lane & 31);
+  const bool tvalid = t < tokens;
+  const float* qrow = q_nope + ((int64_t)(tvalid ? t : 0) * nh + h) * dn + 8 * (lane >> 5);
+  f32x4 qa[8], qb[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    if (NKS > 0 ? ks < NKS : ks < nks) {
+      qa[ks] = *reinterpret_cast<const f32x4*>(qrow + 16 * ks);
+      qb[ks] = *reinterpret_cast<const f32x4*>(qrow + 16 * ks + 4);
+    }
+  }
+  // W_UK[h*dn + i][cb*128 + 0..127] for i < dn, 16 B per thread-load
+  i16x8 wv[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int q = tid + 256 * k;
+    if (NKS > 0 ? k < NKS : q < dn * 16)
+      wv[k] = *reinterpret_cast<const i16x8*>(W + ((int64_t)h * dn + (q >> 4)) * dc + cb * kAbsCols + (q & 15) * 8);
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int q = tid + 256 * k;
+    if (NKS > 0 ? k < NKS : q < dn * 16) *reinterpret_cast<i16x8*>(wt + (q >> 4) * kAbsRowBytes + (q & 15) * 16) = wv[k];
   }
   __syncthreads();
 
-  const int t = t0 + (lane & 31);
-  const bool tvalid = t < tokens;
-  const float* qrow = q_nope + ((int64_t)(tvalid ? t : 0) * nh + h) * dn;
   f32x16 acc_hi = {}, acc_lo = {};
   const int g = lane >> 4, s = lane & 15;
-  for (int ks = 0; ks < dn / 16; ++ks) {
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    if (NKS > 0 ? ks >= NKS : ks >= nks) break;
     float x[8];
-    if (tvalid) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(qrow + 16 * ks + 8 * (lane >> 5));
-      const f32x4 b = *reinterpret_cast<const f32x4*>(qrow + 16 * ks + 8 * (lane >> 5) + 4);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        x[e] = a[e];
-        x[4 + e] = b[e];
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = 0.f;
+    for (int e = 0; e < 4; ++e) {
+      x[e] = tvalid ? qa[ks][e] : 0.f;
+      x[4 + e] = tvalid ? qb[ks][e] : 0.f;
     }
     vec ahi, alo;
     split8<WT>(x, ahi, alo);
@@ -134,13 +155,45 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
     acc_lo = M::mma(alo, b, acc_lo);
   }
   // D[m = token][n = column]
+  const int col = cb * kAbsCols + 32 * wave + (lane & 31);
+  const int prow = dc + dR;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int m = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
     const int tt = t0 + m;
-    if (tt < tokens)
-      q_abs[((int64_t)tt * nh + h) * dc + cb * kAbsCols + 32 * wave + (lane & 31)] =
-          acc_hi[i] + acc_lo[i] * (1.f / M::kLoScale);
+    if (tt >= tokens) continue;
+    const float v = acc_hi[i] + acc_lo[i] * (1.f / M::kLoScale);
+    const int64_t row = (int64_t)tt * nh + h;
+    if (out_mode == 0) reinterpret_cast<float*>(out)[row * dc + col] = v;
+    else if (out_mode == 1) reinterpret_cast<__bf16*>(out)[row * prow + col] = (__bf16)(v * scale);
+    else reinterpret_cast<_Float16*>(out)[row * prow + col] = (_Float16)(v * scale);
+  }
+  if (out_mode != 0 && cb == 0) {
+    // q_rope part of the same rows: 8 elements per thread-step
+    for (int q = tid; q < 32 * (dR / 8); q += 256) {
+      const int tt = t0 + q / (dR / 8), j = 8 * (q % (dR / 8));
+      if (tt >= tokens) continue;
+      const int64_t row = (int64_t)tt * nh + h;
+      const f32x4 a = *reinterpret_cast<const f32x4*>(q_rope + row * dR + j);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(q_rope + row * dR + j + 4);
+      if (out_mode == 1) {
+        bf16x8 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = (__bf16)(a[e] * scale);
+          v[4 + e] = (__bf16)(b[e] * scale);
+        }
+        *reinterpret_cast<bf16x8*>(reinterpret_cast<__bf16*>(out) + row * prow + dc + j) = v;
+      } else {
+        f16x8 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = (_Float16)(a[e] * scale);
+          v[4 + e] = (_Float16)(b[e] * scale);
+        }
+        *reinterpret_cast<f16x8*>(reinterpret_cast<_Float16*>(out) + row * prow + dc + j) = v;
+      }
+    }
   }
 }
 
@@ -225,22 +278,32 @@ __global__ __launch_bounds__(256) void project_mfma_kernel(DecodeProblem p, cons
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int R = p.num_seqs * p.qps;
 
+  // All global loads first: this wave's 8 rows of merged O (rows past R read
+  // row R-1 and are zeroed) and its 32 W_UV operand vectors.
+  f32x4 oa[8], ob[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int r = min(r0 + wave + 4 * k, R - 1);
+    const float* src = o_merged + ((int64_t)r * p.nh + h) * kDcP + 8 * lane;
+    oa[k] = *reinterpret_cast<const f32x4*>(src);
+    ob[k] = *reinterpret_cast<const f32x4*>(src + 4);
+  }
+  const WT* wrow = reinterpret_cast<const WT*>(p.W_UV) + ((int64_t)h * p.dv + 32 * wave + (lane & 31)) * kDcP +
+                   8 * (lane >> 5);
+  vec bw[kDcP / 16];
+#pragma unroll
+  for (int ks = 0; ks < kDcP / 16; ++ks) bw[ks] = __builtin_bit_cast(vec, *reinterpret_cast<const i16x8*>(wrow + 16 * ks));
+
   // ---- phase 1: merged O of 32 rows -> LDS (hi/lo) ----
-  for (int rr = wave; rr < 32; rr += 4) {
-    const int r = r0 + rr;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int rr = wave + 4 * k;
+    const bool ok = r0 + rr < R;
     float o[8];
-    if (r < R) {
-      const float* src = o_merged + ((int64_t)r * p.nh + h) * kDcP + 8 * lane;
-      const f32x4 a = *reinterpret_cast<const f32x4*>(src);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        o[e] = a[e];
-        o[4 + e] = b[e];
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = 0.f;
+    for (int e = 0; e < 4; ++e) {
+      o[e] = ok ? oa[k][e] : 0.f;
+      o[4 + e] = ok ? ob[k][e] : 0.f;
     }
     vec vh, vl;
     split8<WT>(o, vh, vl);
@@ -250,18 +313,15 @@ __global__ __launch_bounds__(256) void project_mfma_kernel(DecodeProblem p, cons
   __syncthreads();
 
   // ---- phase 2: out[token][32w + n] = sum_c O[token][c] * W_UV[h*dv + 32w + n][c] ----
-  const WT* wrow = reinterpret_cast<const WT*>(p.W_UV) + ((int64_t)h * p.dv + 32 * wave + (lane & 31)) * kDcP +
-                   8 * (lane >> 5);
   const char* ah = o_hi + (lane & 31) * kORowBytes + 16 * (lane >> 5);
   const char* al = o_lo + (lane & 31) * kORowBytes + 16 * (lane >> 5);
   f32x16 acc_hi = {}, acc_lo = {};
-#pragma unroll 4
+#pragma unroll
   for (int ks = 0; ks < kDcP / 16; ++ks) {
-    const vec b = __builtin_bit_cast(vec, *reinterpret_cast<const i16x8*>(wrow + 16 * ks));
     const vec a1 = *reinterpret_cast<const vec*>(ah + 32 * ks);
     const vec a2 = *reinterpret_cast<const vec*>(al + 32 * ks);
-    acc_hi = M::mma(a1, b, acc_hi);
-    acc_lo = M::mma(a2, b, acc_lo);
+    acc_hi = M::mma(a1, bw[ks], acc_hi);
+    acc_lo = M::mma(a2, bw[ks], acc_lo);
   }
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -278,15 +338,20 @@ bool absorb_mfma_supported(int w_dtype, int nh, int dn, int dc) {
   return (w_dtype == LA_DTYPE_BF16 || w_dtype == LA_DTYPE_F16) && dn % 16 == 0 && dn <= 128 && dc % kAbsCols == 0;
 }
 
-hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype, float* q_abs, int tokens, int nh,
-                              int dn, int dc, hipStream_t stream) {
+hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype, void* out, int out_mode,
+                              const float* q_rope, float scale, int dR, int tokens, int nh, int dn, int dc,
+                              hipStream_t stream) {
   dim3 grid(nh, dc / kAbsCols, (tokens + 31) / 32);
-  if (w_dtype == LA_DTYPE_BF16)
-    hipLaunchKernelGGL(absorb_mfma_kernel<__hip_bfloat16>, grid, dim3(256), 0, stream, q_nope,
-                       reinterpret_cast<const __hip_bfloat16*>(W_UK), q_abs, tokens, nh, dn, dc);
-  else
-    hipLaunchKernelGGL(absorb_mfma_kernel<__half>, grid, dim3(256), 0, stream, q_nope,
-                       reinterpret_cast<const __half*>(W_UK), q_abs, tokens, nh, dn, dc);
+  const bool d128 = dn == 128;
+  if (w_dtype == LA_DTYPE_BF16) {
+    auto k = d128 ? absorb_mfma_kernel<__hip_bfloat16, 8> : absorb_mfma_kernel<__hip_bfloat16, 0>;
+    hipLaunchKernelGGL(k, grid, dim3(256), 0, stream, q_nope, reinterpret_cast<const __hip_bfloat16*>(W_UK), out,
+                       out_mode, q_rope, scale, dR, tokens, nh, dn, dc);
+  } else {
+    auto k = d128 ? absorb_mfma_kernel<__half, 8> : absorb_mfma_kernel<__half, 0>;
+    hipLaunchKernelGGL(k, grid, dim3(256), 0, stream, q_nope, reinterpret_cast<const __half*>(W_UK), out, out_mode,
+                       q_rope, scale, dR, tokens, nh, dn, dc);
+  }
   return hipGetLastError();
 }
 
