@@ -56,6 +56,7 @@ struct Plan {
   int num_chunks = 0;
   int num_slots = 0;
   bool proj_mfma = false;
+  size_t part_scale_off = 0;
   bool absorb_mfma = false;  // q_nope . W_UK on the MFMA kernel
   bool absorb_prep = false;  // ... writing the attention kernel's 16-bit Q rows directly
   size_t q_abs_off = 0, q_prep_off = 0, part_o_off = 0, part_lse_off = 0, o_merged_off = 0, total = 0;
@@ -153,8 +154,14 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
     pl.q_prep_off = off;
     off += align_up((size_t)a->num_seqs * p->Hq * (c.kv_lora_rank + c.qk_rope_head_dim) * 2);
   }
+  // the MFMA kernel writes its partial rows as scaled fp16, the VALU kernel as fp32
+  p->part_f16 = pl.mfma ? 1 : 0;
   pl.part_o_off = off;
-  off += align_up((size_t)pl.num_slots * p->Hq * c.kv_lora_rank * sizeof(float));
+  off += align_up((size_t)pl.num_slots * p->Hq * c.kv_lora_rank * (pl.mfma ? 2 : 4));
+  if (pl.mfma) {
+    pl.part_scale_off = off;
+    off += align_up((size_t)pl.num_slots * p->Hq * sizeof(float));
+  }
   pl.part_lse_off = off;
   off += align_up((size_t)pl.num_slots * p->Hq * sizeof(float));
   pl.proj_mfma = project_mfma_supported(*p);
@@ -221,6 +228,7 @@ int run(const la_decode_args* a, hipStream_t stream) {
   }
   p.part_o = reinterpret_cast<float*>(ws + plan.part_o_off);
   p.part_lse = reinterpret_cast<float*>(ws + plan.part_lse_off);
+  p.part_scale = plan.mfma ? reinterpret_cast<float*>(ws + plan.part_scale_off) : nullptr;
   if (plan.num_chunks > 0) {
     if (plan.mfma && !plan.absorb_prep) {
       hipError_t e = launch_prep_q(p, stream);

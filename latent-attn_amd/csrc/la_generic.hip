@@ -189,8 +189,8 @@ __global__ __launch_bounds__(kCombineThreads) void combine_project_kernel(Decode
       const int64_t slot = c + s;
       const float w = exp2f(p.part_lse[slot * p.Hq + hq] - M);
       wsum += w;
-      const float* src = p.part_o + (slot * p.Hq + hq) * dc;
-      for (int i = lane; i < dc; i += 64) orow[i] += w * src[i];
+      const int64_t prow = slot * p.Hq + hq;
+      for (int i = lane; i < dc; i += 64) orow[i] += w * load_part(p, prow, i);
     }
     const float inv = 1.f / wsum;
     for (int c = lane; c < dc; c += 64) orow[c] *= inv;

@@ -54,9 +54,17 @@ struct DecodeProblem {
   int chunk_len;
   int num_chunks;
   int num_slots;
-  float* part_o;
+  float* part_o;       // fp32 rows, or fp16 rows when part_f16 (see part_scale)
   float* part_lse;
+  int part_f16;        // 1: part_o holds fp16 rows O * 2^-e, e chosen per row so |.| < 1
+  float* part_scale;   // part_f16: 2^e per (slot, hq), the factor that restores the row
 };
+
+// Partial row (slot, hq) element i as fp32.
+__device__ inline float load_part(const DecodeProblem& p, int64_t row, int i) {
+  if (p.part_f16) return (float)reinterpret_cast<const _Float16*>(p.part_o)[row * p.dc + i] * p.part_scale[row];
+  return p.part_o[row * p.dc + i];
+}
 
 // First row of sequence s, clamped into [0, total_rows] so that malformed
 // offsets can give wrong answers but never out-of-bounds reads.

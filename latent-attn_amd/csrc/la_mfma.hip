@@ -10,9 +10,9 @@
 // The reference computes this on one thread per head; here one workgroup
 // streams a chunk of the cache once for a group of up to 128 heads.
 //
-// Work decomposition. 1-D grid over (chunk, head group); when there are
-// several head groups, the groups of one chunk get block ids 8 apart (same
-// XCD under round-robin dispatch, so re-reads of a tile hit L2). 256 threads
+// Work decomposition. 1-D grid over (chunk, head group), mapped XCD-aware
+// (block_coords): each XCD gets a contiguous range of chunks, so the chunks
+// of one sequence (and the head groups of one chunk) share an L2. 256 threads
 // = 4 waves, one per SIMD; wave w owns heads [32w, 32w+32) of the group. A
 // block walks the segments of its chunk (pieces of the chunk inside one
 // sequence) in tiles of 32 positions:
@@ -37,8 +37,9 @@
 //     accumulator layout already is the A-operand layout of P (lane = head,
 //     8 positions per k-step), so P never goes through LDS; B = tile columns
 //     via ds_read_b64_tr_b16.
-//   * At a segment end O / l and the base-2 log-sum-exp m + log2(l) go to
-//     partial slot (chunk + sequence); la_proj.hip merges the slots.
+//   * At a segment end O / l (fp16, with a power-of-two scale per row) and
+//     the base-2 log-sum-exp m + log2(l) go to partial slot (chunk +
+//     sequence); la_proj.hip merges the slots.
 #include "la_internal.hpp"
 
 #include <hip/hip_ext.h>
@@ -223,13 +224,14 @@ __device__ inline void wait_vm() {
 // The "memory" clobber keeps the compiler from moving LDS accesses across it.
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Returns x through an empty asm: values computed from the result cannot be
-// hoisted out of the enclosing loop. Used on the lane index at the top of each
-// tile so per-lane addresses are recomputed (a few VALU ops) instead of being
-// kept live across the loop in dozens of VGPRs.
-__device__ inline int opaque(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
+// The lane index, computed by a volatile asm (v_mbcnt) at each use: nothing
+// derived from it can be hoisted out of the enclosing loop, so per-lane
+// addresses are recomputed per tile (a few VALU ops) instead of being kept
+// live across the loop (or spilled) in VGPRs.
+__device__ inline int lane_id() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
 }
 
 // LDS is addressed with 32-bit byte offsets from the start of the dynamic LDS
@@ -396,17 +398,19 @@ __device__ inline void rotate_rows(lchar* L, uint32_t buf, int wave, int lane) {
   rot_finish<KT>(L, r);
 }
 
-// Block id -> (chunk, head group).
-__device__ inline void block_coords(int groups, int* chunk, int* group) {
+// Block id -> (chunk, head group), XCD-aware. Workgroups are dispatched
+// round-robin over the 8 XCDs (id % 8), each with its own L2. XCD x gets the
+// contiguous chunk range [x*per, (x+1)*per): the chunks of one sequence share
+// an L2, so the sequence's Q rows are fetched from HBM once per XCD rather than
+// once per chunk, and every XCD streams one contiguous piece of the cache. The
+// head groups of a chunk are adjacent ids on the same XCD. Ids past the last
+// chunk return at once.
+__device__ inline void block_coords(int num_chunks, int groups, int* chunk, int* group) {
   const int id = blockIdx.x;
-  if (groups == 1) {
-    *chunk = id;
-    *group = 0;
-    return;
-  }
+  const int per = (num_chunks + 7) / 8;
   const int x = id & 7, k = id >> 3;
   *group = k % groups;
-  *chunk = (k / groups) * 8 + x;
+  *chunk = x * per + k / groups;
 }
 
 template <typename KT>
@@ -420,7 +424,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
   const int tid = threadIdx.x, lane0 = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keep in SGPRs
   int chunk, group;
-  block_coords(groups, &chunk, &group);
+  block_coords(p.num_chunks, groups, &chunk, &group);
   if (chunk >= p.num_chunks) return;
   const int hg_heads = min(kHG, p.Hq - group * kHG);
   const uint32_t scratch = kScratchOff + 128 * wave;  // per-wave 32 floats
@@ -507,7 +511,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     bool resc_pend = false;    // wave-uniform
     for (int t = -1; t < ntiles; ++t) {
       lds_barrier();  // tile t+1 staged and rotated by every wave; iteration t-1 done
-      const int lane = opaque(tid & 63);
+      const int lane = lane_id();
       const int g2 = lane >> 5;
       const int q16 = lane >> 4, s16 = lane & 15;
       const int head = 32 * wave + (lane & 31);
@@ -703,16 +707,77 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     }
     // register i of block nb: head 8(i/4) + 4*g2 + (i%4), column 32nb + lane%32.
     // Heads come in 16-aligned groups, so validity is uniform per i.
-    float* dst0 = p.part_o + hq0 * kDc + (lane0 & 31);
+    // Rows go out as fp16 O * 2^-e with 2^(e-1) <= max_c |O[c]| < 2^e (so
+    // every value is below 1 in magnitude and keeps 11 significant bits
+    // relative to the row max); 2^e goes to part_scale.
+    f32x16 am = {};
 #pragma unroll
     for (int nb = 0; nb < 16; ++nb) {
-      const f32x16 v = acc[nb] * il16;
+      const f32x16 a = acc[nb];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int hh = 8 * (i >> 2) + 4 * g2 + (i & 3);
-        if (32 * wave + hh < hg_heads) dst0[(int64_t)hh * kDc + 32 * nb] = v[i];
+      for (int i = 0; i < 16; ++i) am[i] = fmaxf(am[i], fabsf(a[i]));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int k = 1; k < 32; k <<= 1)  // over the 32 lanes (columns) of this half
+#pragma unroll
+      for (int i = 0; i < 16; ++i) am[i] = fmaxf(am[i], __shfl_xor(am[i], k, 64));
+    f32x16 mul;
+    float my_scale = 1.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int e = __builtin_amdgcn_frexp_expf(am[i] * il16[i]);  // 0 for a zero row
+      mul[i] = il16[i] * __builtin_amdgcn_ldexpf(1.f, -e);
+      if ((lane0 & 31) == i) my_scale = __builtin_amdgcn_ldexpf(1.f, e);
+    }
+    if ((lane0 & 31) < 16) {
+      const int i = lane0 & 31;
+      const int hh = 8 * (i >> 2) + 4 * g2 + (i & 3);
+      if (32 * wave + hh < hg_heads) p.part_scale[hq0 + hh] = my_scale;
+    }
+    // Write-out through LDS (the tile buffers are idle now): each wave stages
+    // its O^T as fp16 T[column][32 heads] (64-B rows) with 8-B writes of the 4
+    // consecutive heads a lane holds per column, then reads rows of O back with
+    // ds_read_b64_tr_b16 (two reads = 8 columns of one head per lane) and
+    // stores 16 B per lane: 32 stores per lane instead of 256 two-byte ones.
+    lds_barrier();  // every wave has finished with the tile buffers
+    const uint32_t tbase = 32768 * wave;
+#pragma unroll
+    for (int nb = 0; nb < 16; ++nb) {
+      const f32x16 v = acc[nb] * mul;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        i16x4 h4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h4[r] = __builtin_bit_cast(short, (_Float16)v[4 * q + r]);
+        lds_st(L, tbase + (32 * nb + (lane0 & 31)) * 64 + (8 * q + 4 * g2) * 2, h4);
       }
       __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes before its reads
+    {
+      // tr read x of round j: lane (q16, s16) supplies T[r0 + s16/4][c0 + 4(s16%4)]
+      // with r0 = 16j + 8(q16>>1) + 4x, c0 = 16(q16&1); lane i of the group gets
+      // T[r0 + v][c0 + i], v = 0..3, i.e. columns r0..r0+3 of head c0 + i.
+      const int q16 = lane0 >> 4, s16 = lane0 & 15;
+      const int head = 16 * (q16 & 1) + s16;
+      const uint32_t rd = tbase + (8 * (q16 >> 1) + (s16 >> 2)) * 64 + (16 * (q16 & 1) + 4 * (s16 & 3)) * 2;
+      _Float16* dsth = reinterpret_cast<_Float16*>(p.part_o) + (hq0 + head) * kDc + 8 * (q16 >> 1);
+      const bool hok = 32 * wave + head < hg_heads;
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        const i16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)(lds_void*)(L + rd + j * 16 * 64));
+        const i16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)(lds_void*)(L + rd + j * 16 * 64 + 4 * 64));
+        i16x8 row;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          row[e] = x0[e];
+          row[4 + e] = x1[e];
+        }
+        if (hok) *reinterpret_cast<i16x8*>(dsth + 16 * j) = row;
+      }
     }
     lo = seg_hi;
     ++s;
@@ -754,7 +819,7 @@ hipError_t launch_t(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_be
     attr_set = true;
   }
   const int groups = (p.Hq + kHG - 1) / kHG;
-  const int64_t blocks = groups == 1 ? p.num_chunks : (int64_t)((p.num_chunks + 7) / 8) * 8 * groups;
+  const int64_t blocks = (int64_t)((p.num_chunks + 7) / 8) * 8 * groups;
   if (ev_begin || ev_end) {
     // the events time this kernel's execution alone (no dispatch gap)
     hipExtLaunchKernelGGL((decode_mfma_kernel<KT>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, stream,

@@ -27,6 +27,8 @@
 //          read once per block).
 #include "la_internal.hpp"
 
+#include <type_traits>
+
 namespace la {
 namespace {
 
@@ -210,7 +212,27 @@ constexpr int kProjLdsBytes = 2 * 32 * kORowBytes;
 // latent columns 8l .. 8l+7; the slot loads go out 8 at a time.
 constexpr int kMergeWaves = 4;
 
+// One slot's 8 columns of this lane as fp32 (fp16 rows: before the row scale,
+// which the caller folds into the slot weight).
+template <bool F16>
+__device__ inline void load8(const void* rowp, f32x4& a, f32x4& b) {
+  if constexpr (F16) {
+    const f16x8 h = *reinterpret_cast<const f16x8*>(rowp);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[e] = (float)h[e];
+      b[e] = (float)h[4 + e];
+    }
+  } else {
+    a = *reinterpret_cast<const f32x4*>(rowp);
+    b = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(rowp) + 4);
+  }
+}
+
+// F16: partial rows are fp16 with a per-row power-of-two scale (part_scale).
+template <bool F16>
 __global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodeProblem p, float* __restrict__ o_merged) {
+  typedef typename std::conditional<F16, _Float16, float>::type PT;
   const int lane = threadIdx.x & 63;
   const int64_t pair = (int64_t)blockIdx.x * kMergeWaves + (threadIdx.x >> 6);
   const int R = p.num_seqs * p.qps;
@@ -223,8 +245,9 @@ __global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodePro
   if (hi > lo) {
     const int64_t cf = lo / p.chunk_len;
     const int n = (int)((hi - 1) / p.chunk_len - cf + 1);  // slots cf+s .. cf+s+n-1
-    const float* lse = p.part_lse + (cf + s) * p.Hq + hq;
-    const float* src = p.part_o + ((cf + s) * p.Hq + hq) * kDcP + 8 * lane;
+    const int64_t row0 = (cf + s) * p.Hq + hq;
+    const float* lse = p.part_lse + row0;
+    const PT* src = reinterpret_cast<const PT*>(p.part_o) + row0 * kDcP + 8 * lane;
     const int64_t sstride = (int64_t)p.Hq * kDcP;
     float mx = -INFINITY;
     for (int i = lane; i < n; i += 64) mx = fmaxf(mx, lse[(int64_t)i * p.Hq]);
@@ -234,20 +257,17 @@ __global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodePro
       const int nb = min(64, n - i0);
       const float wl = lane < nb ? exp2f(lse[(int64_t)(i0 + lane) * p.Hq] - mx) : 0.f;
       wsum += wave_sum(wl);
+      float wv = wl;  // fp16 rows: the row's power-of-two scale folds into the weight
+      if constexpr (F16) wv = lane < nb ? wl * p.part_scale[row0 + (int64_t)(i0 + lane) * p.Hq] : 0.f;
       for (int j = 0; j < nb; j += 8) {
         f32x4 d0[8], d1[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          if (j + u < nb) {
-            const float* q = src + (int64_t)(i0 + j + u) * sstride;
-            d0[u] = *reinterpret_cast<const f32x4*>(q);
-            d1[u] = *reinterpret_cast<const f32x4*>(q + 4);
-          }
-        }
+        for (int u = 0; u < 8; ++u)
+          if (j + u < nb) load8<F16>(src + (int64_t)(i0 + j + u) * sstride, d0[u], d1[u]);
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           if (j + u < nb) {
-            const float w = __shfl(wl, j + u, 64);
+            const float w = __shfl(wv, j + u, 64);
             o0 += w * d0[u];
             o1 += w * d1[u];
           }
@@ -382,8 +402,11 @@ size_t combine_project_mfma_workspace(const DecodeProblem& p) {
 hipError_t launch_combine_project_mfma(const DecodeProblem& p, float* o_merged, hipStream_t stream) {
   const int64_t pairs = (int64_t)p.num_seqs * p.qps * p.nh;
   if (pairs == 0) return hipSuccess;
-  hipLaunchKernelGGL(merge_slots_kernel, dim3((unsigned)((pairs + kMergeWaves - 1) / kMergeWaves)),
-                     dim3(kMergeWaves * 64), 0, stream, p, o_merged);
+  const dim3 grid((unsigned)((pairs + kMergeWaves - 1) / kMergeWaves));
+  if (p.part_f16)
+    hipLaunchKernelGGL((merge_slots_kernel<true>), grid, dim3(kMergeWaves * 64), 0, stream, p, o_merged);
+  else
+    hipLaunchKernelGGL((merge_slots_kernel<false>), grid, dim3(kMergeWaves * 64), 0, stream, p, o_merged);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.wuv_dtype == LA_DTYPE_BF16) return launch_proj<__hip_bfloat16>(p, o_merged, stream);
