@@ -152,7 +152,7 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   }
   if (pl.mfma) {
     pl.q_prep_off = off;
-    off += align_up((size_t)a->num_seqs * p->Hq * (c.kv_lora_rank + c.qk_rope_head_dim) * 2);
+    off += align_up((size_t)a->num_seqs * qprep_rows_per_seq(p->Hq) * kQPrepRow * 2);
   }
   // the MFMA kernel writes its partial rows as scaled fp16, the VALU kernel as fp32
   p->part_f16 = pl.mfma ? 1 : 0;
@@ -215,11 +215,12 @@ int run(const la_decode_args* a, hipStream_t stream) {
       // absorbed, scaled 16-bit Q rows for the attention kernel in one pass
       e = launch_absorb_mfma(a->q_nope, a->W_UK, a->w_uk_dtype, p.q_prep, p.kv_dtype == LA_DTYPE_BF16 ? 1 : 2,
                              a->q_rope, p.scale_log2, c.qk_rope_head_dim, (int)tokens, c.num_heads,
-                             c.qk_nope_head_dim, c.kv_lora_rank, stream);
+                             c.qk_nope_head_dim, c.kv_lora_rank, a->queries_per_seq, stream);
     } else {
       float* qa = reinterpret_cast<float*>(ws + plan.q_abs_off);
       e = plan.absorb_mfma ? launch_absorb_mfma(a->q_nope, a->W_UK, a->w_uk_dtype, qa, 0, nullptr, 1.f, 0,
-                                                (int)tokens, c.num_heads, c.qk_nope_head_dim, c.kv_lora_rank, stream)
+                                                (int)tokens, c.num_heads, c.qk_nope_head_dim, c.kv_lora_rank, 1,
+                                                stream)
                            : launch_absorb(a->q_nope, a->W_UK, a->w_uk_dtype, qa, (int)tokens, c.num_heads,
                                            c.qk_nope_head_dim, c.kv_lora_rank, stream);
       p.q_abs = qa;
@@ -355,7 +356,7 @@ int la_absorb_q(const float* q_nope, const void* W_UK, int w_uk_dtype, float* q_
   const bool mfma = la::absorb_mfma_supported(w_uk_dtype, cfg->num_heads, cfg->qk_nope_head_dim, cfg->kv_lora_rank) &&
                     (reinterpret_cast<uintptr_t>(q_nope) & 15) == 0 && (reinterpret_cast<uintptr_t>(W_UK) & 15) == 0;
   hipError_t e = mfma ? la::launch_absorb_mfma(q_nope, W_UK, w_uk_dtype, q_absorbed, 0, nullptr, 1.f, 0, tokens,
-                                               cfg->num_heads, cfg->qk_nope_head_dim, cfg->kv_lora_rank,
+                                               cfg->num_heads, cfg->qk_nope_head_dim, cfg->kv_lora_rank, 1,
                                                static_cast<hipStream_t>(stream))
                       : la::launch_absorb(q_nope, W_UK, w_uk_dtype, q_absorbed, tokens, cfg->num_heads,
                                           cfg->qk_nope_head_dim, cfg->kv_lora_rank, static_cast<hipStream_t>(stream));

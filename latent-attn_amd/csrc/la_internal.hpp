@@ -27,6 +27,18 @@ constexpr float kLog2e = 1.4426950408889634f;
 // log-sum-exp of the scaled scores). Slots are unique because a sequence's
 // chunks form a contiguous range that starts no earlier than where the
 // previous sequence's range ends; num_slots = num_chunks + num_seqs - 1.
+// q_prep layout of the MFMA path ("operand order"). The query rows of each
+// sequence are padded to a multiple of 32 (qprep_rows_per_seq) and cut into
+// blocks of 32 rows (qrow = s * qprep_rows_per_seq(Hq) + hq). Block b stores,
+// for k-step kk (16 elements of the 576-element row) and lane l = r + 32 g,
+// the 8 elements Q[32 b + r][16 kk + 8 g .. +8] at element 512 kk + 8 l: the
+// attention kernel's B operand of k-step kk is one coalesced 1 KB load.
+constexpr int kQPrepRow = 576;  // kv_lora_rank 512 + qk_rope_head_dim 64
+__host__ __device__ inline int qprep_rows_per_seq(int Hq) { return (Hq + 31) & ~31; }
+__host__ __device__ inline int64_t qprep_index(int64_t qrow, int c) {
+  return (qrow >> 5) * (32 * kQPrepRow) + 512 * (c >> 4) + 8 * ((qrow & 31) + 32 * ((c >> 3) & 1)) + (c & 7);
+}
+
 struct DecodeProblem {
   const void* kv;
   int kv_dtype;
@@ -40,8 +52,9 @@ struct DecodeProblem {
   int Hq;                 // query heads per sequence = qps * nh
   const float* q_abs;     // (num_seqs*Hq, dc) f32
   const float* q_rope;    // (num_seqs*Hq, dR) f32
-  void* q_prep;           // MFMA path: (num_seqs*Hq, dc + dR) in the cache's 16-bit type,
-                          // [q_abs | q_rope] * scale_log2, written by launch_prep_q
+  void* q_prep;           // MFMA path: [q_abs | q_rope] * scale_log2 in the cache's 16-bit
+                          // type, operand-order layout (qprep_index), written by
+                          // launch_prep_q or the absorb kernel
   const void* W_UV;
   int wuv_dtype;
   const float* rope_cos;
@@ -142,10 +155,12 @@ hipError_t launch_combine_project(const DecodeProblem& p, hipStream_t stream);
 
 // MFMA versions for 16-bit weights (la_proj.hip).
 bool absorb_mfma_supported(int w_dtype, int nh, int dn, int dc);
-// out_mode 0: out = q_abs (fp32). 1 / 2: out = q_prep rows (bf16 / fp16) =
-// [q_abs | q_rope] * scale, as prep_q_kernel writes them.
+// out_mode 0: out = q_abs (fp32). 1 / 2: out = q_prep (bf16 / fp16) =
+// [q_abs | q_rope] * scale in the operand-order layout, as prep_q_kernel
+// writes it; token t is query t % qps of sequence t / qps (qps = tokens per
+// sequence, used by modes 1 / 2 only).
 hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype, void* out, int out_mode,
-                              const float* q_rope, float scale, int dR, int tokens, int nh, int dn, int dc,
+                              const float* q_rope, float scale, int dR, int tokens, int nh, int dn, int dc, int qps,
                               hipStream_t stream);
 bool project_mfma_supported(const DecodeProblem& p);
 // Workspace bytes for the merged O (fp32, (num_seqs*Hq, dc)) the MFMA

@@ -64,7 +64,7 @@ constexpr int kSinOff = kCosOff + kT * 128;  // sin rows
 constexpr int kBufBytes = kSinOff + kT * 128;  // 45056
 constexpr int kNBuf = 3;
 constexpr int kScratchOff = kNBuf * kBufBytes;  // per-wave 32 floats
-constexpr int kQropeOff = kScratchOff + kWaves * 32 * 4;  // q_rope of the group: 128 rows x 128 B
+constexpr int kQropeOff = kScratchOff + kWaves * 32 * 4;  // q rope k-steps: [wave][r][lane] 16 B
 constexpr int kLdsBytes = kQropeOff + kHG * kDr * 2;
 constexpr int kDmaPerWave = 11;        // 8 c_t rows + k_rope + cos + sin
 constexpr int kRescaleSlack = 8;       // log2 units before the running max moves
@@ -232,6 +232,37 @@ __device__ inline int lane_id() {
   int l;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
   return l;
+}
+
+// Cross-lane combines without a lane index (no ds_bpermute: no LDS counter
+// traffic and no lane-id register to keep live). permlane32_swap(x, x)
+// returns (x[l % 32], x[l % 32 + 32]) in every lane l, permlane16_swap(x, x)
+// the same for 16-lane halves of each 32-lane half; DPP 0xB1 / 0x4E / 0x141
+// / 0x140 read lane l^1 / l^2 / the mirror inside 8 / inside 16 lanes.
+__device__ inline float f_of(unsigned u) { return __builtin_bit_cast(float, u); }
+__device__ inline unsigned u_of(float f) { return __builtin_bit_cast(unsigned, f); }
+// x[l] + x[l ^ 32]
+__device__ inline float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(u_of(x), u_of(x), false, false);
+  return f_of(r[0]) + f_of(r[1]);
+}
+// max of x over lanes l^32
+__device__ inline float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(u_of(x), u_of(x), false, false);
+  return fmaxf(f_of(r[0]), f_of(r[1]));
+}
+template <int CTRL>
+__device__ inline float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+// max of x over the 32 lanes of this lane's half of the wave
+__device__ inline float max32(float x) {
+  x = fmaxf(x, dpp_f<0xB1>(x));
+  x = fmaxf(x, dpp_f<0x4E>(x));
+  x = fmaxf(x, dpp_f<0x141>(x));
+  x = fmaxf(x, dpp_f<0x140>(x));
+  const auto r = __builtin_amdgcn_permlane16_swap(u_of(x), u_of(x), false, false);
+  return fmaxf(f_of(r[0]), f_of(r[1]));
 }
 
 // LDS is addressed with 32-bit byte offsets from the start of the dynamic LDS
@@ -452,37 +483,38 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
 
     lds_barrier();  // all waves are done with the previous segment's buffers
 
-    issue_tile_dma(p, sg, 0, L, 0, wave, lane0);  // tile 1 rides along iteration -1
+    // tile 1 rides along iteration -1; a fresh lane index keeps the per-lane
+    // addresses out of the registers (and spill slots) that live across the
+    // prologue: a spill reload here would wait on vmcnt and so serialise the copies
+    issue_tile_dma(p, sg, 0, L, 0, wave, lane_id());
 
     // Q^T as the B operand: lane holds Q[head][16kk + 8*g2 .. +8], pre-scaled.
-    // The 32 latent k-steps stay in VGPRs; the 4 rope k-steps go to this
-    // wave's rows of an LDS table (row = head, 16-B chunk j at j ^ fr(head))
-    // to save 16 VGPRs.
+    // q_prep is stored in operand order (qprep_index): the wave's 32 rows form
+    // one block and k-step kk is the coalesced 1 KB at element 512kk. The 32
+    // latent k-steps are loaded into VGPRs; the 4 rope k-steps are copied
+    // straight into this wave's 4 KB of the LDS q-rope table (k-step 32 + r at
+    // 1024r, 16 B per lane) to save 16 VGPRs. A wave without valid heads reads
+    // the group's last block (in bounds); lanes of invalid heads are zeroed,
+    // in VGPRs here and in LDS once the copies have landed.
     vec qb[32];
+    const bool q_head_ok = 32 * wave + (lane0 & 31) < hg_heads;
     {
-      // 16-bit Q rows prepared by prep_q_kernel: all 36 loads go out at once
-      const int g2 = lane0 >> 5;
-      const int head = 32 * wave + (lane0 & 31);
-      const bool head_ok = head < hg_heads;
-      const int64_t qrow = (int64_t)s * p.Hq + group * kHG + (head_ok ? head : 0);
-      const vec* qsrc = reinterpret_cast<const vec*>(reinterpret_cast<const E*>(p.q_prep) + qrow * (kDc + kDr) + 8 * g2);
-      vec qr4[4];
+      const int q_lane = lane_id();
+      const int wblk = min(32 * wave, (hg_heads - 1) & ~31);
+      const int64_t qrow0 = (int64_t)s * qprep_rows_per_seq(p.Hq) + group * kHG + wblk;
+      const E* qbase = reinterpret_cast<const E*>(p.q_prep) + qprep_index(qrow0, 0);
+      static_for<4>([&](auto r_c) {
+        constexpr int r = decltype(r_c)::value;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(qbase) + 1024 * (32 + r) + 16 * q_lane,
+                                         (lds_void*)(L + kQropeOff + 4096 * wave + 1024 * r), 16, 0, 0);
+      });
+      const vec* qsrc = reinterpret_cast<const vec*>(qbase) + q_lane;
 #pragma unroll
-      for (int kk = 0; kk < 36; ++kk) {
-        const vec v = qsrc[2 * kk];
-        if (kk < 32) qb[kk] = v;
-        else qr4[kk - 32] = v;
-      }
+      for (int kk = 0; kk < 32; ++kk) qb[kk] = qsrc[64 * kk];
       const vec zero = {};
 #pragma unroll
-      for (int kk = 0; kk < 36; ++kk) {
-        if (kk < 32) {
-          if (!head_ok) qb[kk] = zero;
-        } else {
-          const int j = 2 * (kk - 32) + g2;
-          lds_st(L, kQropeOff + head * 128 + ((j ^ fr(head)) << 4), head_ok ? qr4[kk - 32] : zero);
-        }
-      }
+      for (int kk = 0; kk < 32; ++kk)
+        if (!q_head_ok) qb[kk] = zero;
     }
 
     float m_run = -INFINITY, l_run = 0.f;
@@ -494,7 +526,12 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     acc_ready(acc);
 
     wait_vm<0>();
-    rotate_rows<KT>(L, 0, wave, lane0);
+    if (!q_head_ok) {
+      const vec zero = {};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lds_st(L, kQropeOff + 4096 * wave + 1024 * r + 16 * lane0, zero);
+    }
+    rotate_rows<KT>(L, 0, wave, lane_id());  // fresh lane index: no spilled addresses
 
     // Software pipeline over tiles; iteration t (from -1):
     //   [apply the O rescale decided by softmax(t)]
@@ -557,7 +594,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       const int arow = lane & 31;
       const uint32_t ct_x = (nxt + arow * 1024) | (16 * (g2 ^ fc(arow)));
       const uint32_t rp_x = (nxt + kRopeOff + arow * 128) | (16 * (g2 ^ fr(arow)));
-      const uint32_t qr_x = (kQropeOff + head * 128) | (16 * (g2 ^ fr(head)));
+      const uint32_t qr_x = kQropeOff + 4096 * wave + 16 * lane;
       auto a_off = [&](int kk) -> uint32_t { return kk < 32 ? (ct_x ^ (32 * kk)) : (rp_x ^ (32 * (kk - 32))); };
 
       // PV(t) value reads: lane (q16, s16), read x of step (ks, nb) supplies
@@ -588,7 +625,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         constexpr int D = kQkDepth;
         if constexpr (kk == kQrAt) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) qr[r] = lds_rd128<vec>(L, qr_x ^ (32 * r));
+          for (int r = 0; r < 4; ++r) qr[r] = lds_rd128<vec>(L, qr_x + 1024 * r);
         }
         vec& a = ar[kk % D];
         wait_lgkm<qk_later(kk)>(a);
@@ -635,7 +672,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           lmax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
           const bool need = sm && lmax > m_run + (float)kRescaleSlack;
           if (__builtin_amdgcn_ballot_w64(need) != 0) {
-            const float tmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
+            const float tmax = max_halves(lmax);
             const float m_new = fmaxf(m_run, tmax);
             const bool first = m_run == -INFINITY;
             const float alpha = first ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -689,13 +726,14 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
 
     // ---- segment end: l over both lane halves; normalise; write the slot ----
     settle_acc(acc);
-    const int g2 = lane0 >> 5;
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const int le = lane_id();  // fresh: the prologue's lane index would come back from a spill slot
+    const int g2 = le >> 5;
+    const float l_tot = sum_halves(l_run);
     const int64_t slot = (int64_t)chunk + s;
     const int64_t hq0 = slot * p.Hq + group * kHG + 32 * wave;
-    if (lane0 < 32) {
-      lds_st(L, scratch + 4 * lane0, 1.f / l_tot);
-      if (32 * wave + lane0 < hg_heads) p.part_lse[hq0 + lane0] = m_run + log2f(l_tot);
+    if (le < 32) {
+      lds_st(L, scratch + 4 * le, 1.f / l_tot);
+      if (32 * wave + le < hg_heads) p.part_lse[hq0 + le] = m_run + log2f(l_tot);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);
     f32x16 il16;
@@ -719,19 +757,17 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int k = 1; k < 32; k <<= 1)  // over the 32 lanes (columns) of this half
-#pragma unroll
-      for (int i = 0; i < 16; ++i) am[i] = fmaxf(am[i], __shfl_xor(am[i], k, 64));
+    for (int i = 0; i < 16; ++i) am[i] = max32(am[i]);  // over the 32 lanes (columns) of this half
     f32x16 mul;
     float my_scale = 1.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int e = __builtin_amdgcn_frexp_expf(am[i] * il16[i]);  // 0 for a zero row
       mul[i] = il16[i] * __builtin_amdgcn_ldexpf(1.f, -e);
-      if ((lane0 & 31) == i) my_scale = __builtin_amdgcn_ldexpf(1.f, e);
+      if ((le & 31) == i) my_scale = __builtin_amdgcn_ldexpf(1.f, e);
     }
-    if ((lane0 & 31) < 16) {
-      const int i = lane0 & 31;
+    if ((le & 31) < 16) {
+      const int i = le & 31;
       const int hh = 8 * (i >> 2) + 4 * g2 + (i & 3);
       if (32 * wave + hh < hg_heads) p.part_scale[hq0 + hh] = my_scale;
     }
@@ -750,7 +786,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         i16x4 h4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) h4[r] = __builtin_bit_cast(short, (_Float16)v[4 * q + r]);
-        lds_st(L, tbase + (32 * nb + (lane0 & 31)) * 64 + (8 * q + 4 * g2) * 2, h4);
+        lds_st(L, tbase + (32 * nb + (le & 31)) * 64 + (8 * q + 4 * g2) * 2, h4);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -759,7 +795,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // tr read x of round j: lane (q16, s16) supplies T[r0 + s16/4][c0 + 4(s16%4)]
       // with r0 = 16j + 8(q16>>1) + 4x, c0 = 16(q16&1); lane i of the group gets
       // T[r0 + v][c0 + i], v = 0..3, i.e. columns r0..r0+3 of head c0 + i.
-      const int q16 = lane0 >> 4, s16 = lane0 & 15;
+      const int q16 = le >> 4, s16 = le & 15;
       const int head = 16 * (q16 & 1) + s16;
       const uint32_t rd = tbase + (8 * (q16 >> 1) + (s16 >> 2)) * 64 + (16 * (q16 & 1) + 4 * (s16 & 3)) * 2;
       _Float16* dsth = reinterpret_cast<_Float16*>(p.part_o) + (hq0 + head) * kDc + 8 * (q16 >> 1);
@@ -784,12 +820,13 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
   }
 }
 
-// q_prep[row] = E([q_abs[row] (dc) | q_rope[row] (dR)] * scale_log2); one
-// thread per 8 consecutive elements (72 per row for dc = 512, dR = 64).
+// q_prep = E([q_abs[row] (dc) | q_rope[row] (dR)] * scale_log2) in the
+// operand-order layout (qprep_index); row = s * Hq + hq. One thread per 8
+// consecutive elements (72 per row for dc = 512, dR = 64), i.e. per 16-B slot.
 template <typename KT>
 __global__ __launch_bounds__(256) void prep_q_kernel(const float* __restrict__ q_abs, const float* __restrict__ q_rope,
-                                                     float scale, typename Ops<KT>::vec* __restrict__ out,
-                                                     int64_t rows) {
+                                                     float scale, typename Ops<KT>::elem* __restrict__ out,
+                                                     int64_t rows, int Hq) {
   typedef typename Ops<KT>::elem E;
   typedef typename Ops<KT>::vec vec;
   constexpr int kPer = (kDc + kDr) / 8;
@@ -806,7 +843,8 @@ __global__ __launch_bounds__(256) void prep_q_kernel(const float* __restrict__ q
     v[e] = (E)(a[e] * scale);
     v[4 + e] = (E)(b[e] * scale);
   }
-  out[i] = v;
+  const int64_t qrow = (row / Hq) * qprep_rows_per_seq(Hq) + row % Hq;
+  *reinterpret_cast<vec*>(out + qprep_index(qrow, 8 * j)) = v;
 }
 
 template <typename KT>
@@ -870,10 +908,10 @@ hipError_t launch_prep_q(const DecodeProblem& p, hipStream_t stream) {
   const unsigned blocks = (unsigned)((threads + 255) / 256);
   if (p.kv_dtype == LA_DTYPE_BF16)
     hipLaunchKernelGGL(prep_q_kernel<__hip_bfloat16>, dim3(blocks), dim3(256), 0, stream, p.q_abs, p.q_rope,
-                       p.scale_log2, reinterpret_cast<Ops<__hip_bfloat16>::vec*>(p.q_prep), rows);
+                       p.scale_log2, reinterpret_cast<Ops<__hip_bfloat16>::elem*>(p.q_prep), rows, p.Hq);
   else
     hipLaunchKernelGGL(prep_q_kernel<__half>, dim3(blocks), dim3(256), 0, stream, p.q_abs, p.q_rope, p.scale_log2,
-                       reinterpret_cast<Ops<__half>::vec*>(p.q_prep), rows);
+                       reinterpret_cast<Ops<__half>::elem*>(p.q_prep), rows, p.Hq);
   return hipGetLastError();
 }
 

@@ -38,6 +38,8 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 template <typename WT>
@@ -92,25 +94,30 @@ template <typename WT, int NKS>
 __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restrict__ q_nope, const WT* __restrict__ W,
                                                           void* __restrict__ out, int out_mode,
                                                           const float* __restrict__ q_rope, float scale, int dR,
-                                                          int tokens, int nh, int dn, int dc) {
+                                                          int tokens, int nh, int dn, int dc, int qps) {
   typedef Mma<WT> M;
   typedef typename M::vec vec;
   __shared__ __attribute__((aligned(16))) char wt[128 * kAbsRowBytes];  // dn <= 128 rows
+  // q operands (hi, lo) of the 8 k-steps, shared by the 4 waves: [ks][hi|lo][lane] 16 B
+  __shared__ __attribute__((aligned(16))) char qs[8 * 2 * 64 * 16];
   const int h = blockIdx.x, cb = blockIdx.y, t0 = blockIdx.z * 32;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int nks = NKS > 0 ? NKS : dn / 16;  // <= 8
   if (NKS > 0) dn = 16 * NKS;
 
-  // q_nope of token t0 + lane%32, elements 16ks + 8(lane/32) .. +8, all k-steps
+  // q_nope of token t0 + lane%32, elements 16ks + 8(lane/32) .. +8: wave w
+  // loads k-steps 2w and 2w+1, splits them into hi/lo 16-bit operands and
+  // stages them in LDS for all waves (each wave issues 4 q loads, not 16)
   const int t = t0 + (lane & 31);
   const bool tvalid = t < tokens;
   const float* qrow = q_nope + ((int64_t)(tvalid ? t : 0) * nh + h) * dn + 8 * (lane >> 5);
-  f32x4 qa[8], qb[8];
+  f32x4 qa[2], qb[2];
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {
-    if (NKS > 0 ? ks < NKS : ks < nks) {
-      qa[ks] = *reinterpret_cast<const f32x4*>(qrow + 16 * ks);
-      qb[ks] = *reinterpret_cast<const f32x4*>(qrow + 16 * ks + 4);
+  for (int j = 0; j < 2; ++j) {
+    const int ks = 2 * wave + j;
+    if (ks < nks) {
+      qa[j] = *reinterpret_cast<const f32x4*>(qrow + 16 * ks);
+      qb[j] = *reinterpret_cast<const f32x4*>(qrow + 16 * ks + 4);
     }
   }
   // W_UK[h*dn + i][cb*128 + 0..127] for i < dn, 16 B per thread-load
@@ -126,6 +133,22 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
     const int q = tid + 256 * k;
     if (NKS > 0 ? k < NKS : q < dn * 16) *reinterpret_cast<i16x8*>(wt + (q >> 4) * kAbsRowBytes + (q & 15) * 16) = wv[k];
   }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int ks = 2 * wave + j;
+    if (ks < nks) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = tvalid ? qa[j][e] : 0.f;
+        x[4 + e] = tvalid ? qb[j][e] : 0.f;
+      }
+      vec hi, lo;
+      split8<WT>(x, hi, lo);
+      *reinterpret_cast<vec*>(qs + (2 * ks) * 1024 + 16 * lane) = hi;
+      *reinterpret_cast<vec*>(qs + (2 * ks + 1) * 1024 + 16 * lane) = lo;
+    }
+  }
   __syncthreads();
 
   f32x16 acc_hi = {}, acc_lo = {};
@@ -133,14 +156,8 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
     if (NKS > 0 ? ks >= NKS : ks >= nks) break;
-    float x[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      x[e] = tvalid ? qa[ks][e] : 0.f;
-      x[4 + e] = tvalid ? qb[ks][e] : 0.f;
-    }
-    vec ahi, alo;
-    split8<WT>(x, ahi, alo);
+    const vec ahi = *reinterpret_cast<const vec*>(qs + (2 * ks) * 1024 + 16 * lane);
+    const vec alo = *reinterpret_cast<const vec*>(qs + (2 * ks + 1) * 1024 + 16 * lane);
     // B[k = i][n = c]: rows 16ks + 8(g>>1) + 4hf + (s>>2), columns 32w + 16(g&1) + 4(s&3)
     i16x8 bv;
 #pragma unroll
@@ -153,31 +170,50 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
       for (int e = 0; e < 4; ++e) bv[4 * hf + e] = r[e];
     }
     const vec b = __builtin_bit_cast(vec, bv);
-    acc_hi = M::mma(ahi, b, acc_hi);
-    acc_lo = M::mma(alo, b, acc_lo);
+    // D^T = W^T . q^T: the W tile is the A operand (lane = column), q the B
+    // operand (lane = token), so each lane ends up with runs of 4 columns
+    acc_hi = M::mma(b, ahi, acc_hi);
+    acc_lo = M::mma(b, alo, acc_lo);
   }
-  // D[m = token][n = column]
-  const int col = cb * kAbsCols + 32 * wave + (lane & 31);
-  const int prow = dc + dR;
+  // D^T[m = column][n = token]: register 4q + r holds column 32w + 8q + 4(lane/32) + r
+  // of token t0 + lane%32, so one 16-byte (fp32) or 8-byte (16-bit) store per q.
+  const int tt = t0 + (lane & 31);
+  if (tt < tokens) {
+    const int col0 = cb * kAbsCols + 32 * wave + 4 * (lane >> 5);
+    // q_prep row of token tt: query tt % qps of sequence tt / qps, weight head h
+    const int64_t qrow = out_mode != 0 ? (int64_t)(tt / qps) * qprep_rows_per_seq(qps * nh) + (tt % qps) * nh + h : 0;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int m = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-    const int tt = t0 + m;
-    if (tt >= tokens) continue;
-    const float v = acc_hi[i] + acc_lo[i] * (1.f / M::kLoScale);
-    const int64_t row = (int64_t)tt * nh + h;
-    if (out_mode == 0) reinterpret_cast<float*>(out)[row * dc + col] = v;
-    else if (out_mode == 1) reinterpret_cast<__bf16*>(out)[row * prow + col] = (__bf16)(v * scale);
-    else reinterpret_cast<_Float16*>(out)[row * prow + col] = (_Float16)(v * scale);
+    for (int q = 0; q < 4; ++q) {
+      f32x4 v;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = acc_hi[4 * q + r] + acc_lo[4 * q + r] * (1.f / M::kLoScale);
+      const int col = col0 + 8 * q;
+      if (out_mode == 0) {
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + ((int64_t)tt * nh + h) * dc + col) = v;
+      } else if (out_mode == 1) {
+        bf16x4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = (__bf16)(v[r] * scale);
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(out) + qprep_index(qrow, col)) = o;
+      } else {
+        f16x4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = (_Float16)(v[r] * scale);
+        *reinterpret_cast<f16x4*>(reinterpret_cast<_Float16*>(out) + qprep_index(qrow, col)) = o;
+      }
+    }
   }
+  const int hq_pad = out_mode != 0 ? qprep_rows_per_seq(qps * nh) : 0;
+  auto qrow_of = [&](int t) -> int64_t { return (int64_t)(t / qps) * hq_pad + (int64_t)(t % qps) * nh + h; };
   if (out_mode != 0 && cb == 0) {
-    // q_rope part of the same rows: 8 elements per thread-step
+    // q_rope part of the same rows: 8 elements (one 16-B slot of q_prep) per thread-step
     for (int q = tid; q < 32 * (dR / 8); q += 256) {
-      const int tt = t0 + q / (dR / 8), j = 8 * (q % (dR / 8));
-      if (tt >= tokens) continue;
-      const int64_t row = (int64_t)tt * nh + h;
+      const int tr = t0 + q / (dR / 8), j = 8 * (q % (dR / 8));
+      if (tr >= tokens) continue;
+      const int64_t row = (int64_t)tr * nh + h;
       const f32x4 a = *reinterpret_cast<const f32x4*>(q_rope + row * dR + j);
       const f32x4 b = *reinterpret_cast<const f32x4*>(q_rope + row * dR + j + 4);
+      const int64_t dst = qprep_index(qrow_of(tr), dc + j);
       if (out_mode == 1) {
         bf16x8 v;
 #pragma unroll
@@ -185,7 +221,7 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
           v[e] = (__bf16)(a[e] * scale);
           v[4 + e] = (__bf16)(b[e] * scale);
         }
-        *reinterpret_cast<bf16x8*>(reinterpret_cast<__bf16*>(out) + row * prow + dc + j) = v;
+        *reinterpret_cast<bf16x8*>(reinterpret_cast<__bf16*>(out) + dst) = v;
       } else {
         f16x8 v;
 #pragma unroll
@@ -193,7 +229,7 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
           v[e] = (_Float16)(a[e] * scale);
           v[4 + e] = (_Float16)(b[e] * scale);
         }
-        *reinterpret_cast<f16x8*>(reinterpret_cast<_Float16*>(out) + row * prow + dc + j) = v;
+        *reinterpret_cast<f16x8*>(reinterpret_cast<_Float16*>(out) + dst) = v;
       }
     }
   }
@@ -212,22 +248,35 @@ constexpr int kProjLdsBytes = 2 * 32 * kORowBytes;
 // latent columns 8l .. 8l+7; the slot loads go out 8 at a time.
 constexpr int kMergeWaves = 4;
 
-// One slot's 8 columns of this lane as fp32 (fp16 rows: before the row scale,
-// which the caller folds into the slot weight).
+// One slot's 8 columns of this lane, kept in the stored format until use
+// (fp16 rows: before the row scale, which the caller folds into the slot
+// weight), so 8 slots in flight cost 32 VGPRs for fp16 rows.
 template <bool F16>
-__device__ inline void load8(const void* rowp, f32x4& a, f32x4& b) {
-  if constexpr (F16) {
-    const f16x8 h = *reinterpret_cast<const f16x8*>(rowp);
+struct SlotRow;
+template <>
+struct SlotRow<true> {
+  f16x8 h;
+  __device__ void load(const void* rowp) { h = *reinterpret_cast<const f16x8*>(rowp); }
+  __device__ void fma(float w, f32x4& o0, f32x4& o1) const {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      a[e] = (float)h[e];
-      b[e] = (float)h[4 + e];
+      o0[e] += w * (float)h[e];
+      o1[e] += w * (float)h[4 + e];
     }
-  } else {
+  }
+};
+template <>
+struct SlotRow<false> {
+  f32x4 a, b;
+  __device__ void load(const void* rowp) {
     a = *reinterpret_cast<const f32x4*>(rowp);
     b = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(rowp) + 4);
   }
-}
+  __device__ void fma(float w, f32x4& o0, f32x4& o1) const {
+    o0 += w * a;
+    o1 += w * b;
+  }
+};
 
 // F16: partial rows are fp16 with a per-row power-of-two scale (part_scale).
 template <bool F16>
@@ -249,29 +298,40 @@ __global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodePro
     const float* lse = p.part_lse + row0;
     const PT* src = reinterpret_cast<const PT*>(p.part_o) + row0 * kDcP + 8 * lane;
     const int64_t sstride = (int64_t)p.Hq * kDcP;
-    float mx = -INFINITY;
-    for (int i = lane; i < n; i += 64) mx = fmaxf(mx, lse[(int64_t)i * p.Hq]);
+    // The first 8 slot rows go out before the log-sum-exps they are weighted
+    // by, so a merge of up to 8 slots takes one memory round trip.
+    SlotRow<F16> d[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (u < n) d[u].load(src + (int64_t)u * sstride);
+    // lane i holds slot i of each 64-slot chunk; chunk 0 stays in registers
+    const float ls0 = lane < n ? lse[(int64_t)lane * p.Hq] : -INFINITY;
+    const float sc0 = F16 && lane < n ? p.part_scale[row0 + (int64_t)lane * p.Hq] : 1.f;
+    float mx = ls0;
+    for (int i = lane + 64; i < n; i += 64) mx = fmaxf(mx, lse[(int64_t)i * p.Hq]);
     mx = wave_max(mx);
     float wsum = 0.f;
     for (int i0 = 0; i0 < n; i0 += 64) {
       const int nb = min(64, n - i0);
-      const float wl = lane < nb ? exp2f(lse[(int64_t)(i0 + lane) * p.Hq] - mx) : 0.f;
+      float wl, sc;
+      if (i0 == 0) {
+        wl = lane < nb ? exp2f(ls0 - mx) : 0.f;
+        sc = sc0;
+      } else {
+        wl = lane < nb ? exp2f(lse[(int64_t)(i0 + lane) * p.Hq] - mx) : 0.f;
+        sc = F16 && lane < nb ? p.part_scale[row0 + (int64_t)(i0 + lane) * p.Hq] : 1.f;
+      }
       wsum += wave_sum(wl);
-      float wv = wl;  // fp16 rows: the row's power-of-two scale folds into the weight
-      if constexpr (F16) wv = lane < nb ? wl * p.part_scale[row0 + (int64_t)(i0 + lane) * p.Hq] : 0.f;
+      const float wv = wl * sc;  // fp16 rows: the row's power-of-two scale folds into the weight
       for (int j = 0; j < nb; j += 8) {
-        f32x4 d0[8], d1[8];
+        if (i0 > 0 || j > 0) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (j + u < nb) d[u].load(src + (int64_t)(i0 + j + u) * sstride);
+        }
 #pragma unroll
         for (int u = 0; u < 8; ++u)
-          if (j + u < nb) load8<F16>(src + (int64_t)(i0 + j + u) * sstride, d0[u], d1[u]);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          if (j + u < nb) {
-            const float w = __shfl(wv, j + u, 64);
-            o0 += w * d0[u];
-            o1 += w * d1[u];
-          }
-        }
+          if (j + u < nb) d[u].fma(__shfl(wv, j + u, 64), o0, o1);
       }
     }
     const float inv = 1.f / wsum;
@@ -359,18 +419,19 @@ bool absorb_mfma_supported(int w_dtype, int nh, int dn, int dc) {
 }
 
 hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype, void* out, int out_mode,
-                              const float* q_rope, float scale, int dR, int tokens, int nh, int dn, int dc,
+                              const float* q_rope, float scale, int dR, int tokens, int nh, int dn, int dc, int qps,
                               hipStream_t stream) {
+  if (out_mode != 0 && (dc + dR != kQPrepRow || qps <= 0)) return hipErrorInvalidValue;
   dim3 grid(nh, dc / kAbsCols, (tokens + 31) / 32);
   const bool d128 = dn == 128;
   if (w_dtype == LA_DTYPE_BF16) {
     auto k = d128 ? absorb_mfma_kernel<__hip_bfloat16, 8> : absorb_mfma_kernel<__hip_bfloat16, 0>;
     hipLaunchKernelGGL(k, grid, dim3(256), 0, stream, q_nope, reinterpret_cast<const __hip_bfloat16*>(W_UK), out,
-                       out_mode, q_rope, scale, dR, tokens, nh, dn, dc);
+                       out_mode, q_rope, scale, dR, tokens, nh, dn, dc, qps);
   } else {
     auto k = d128 ? absorb_mfma_kernel<__half, 8> : absorb_mfma_kernel<__half, 0>;
     hipLaunchKernelGGL(k, grid, dim3(256), 0, stream, q_nope, reinterpret_cast<const __half*>(W_UK), out, out_mode,
-                       q_rope, scale, dR, tokens, nh, dn, dc);
+                       q_rope, scale, dR, tokens, nh, dn, dc, qps);
   }
   return hipGetLastError();
 }

@@ -225,3 +225,50 @@ def test_extension_checks_on_device(cuda):
                              128)
     with pytest.raises(RuntimeError, match="rope_cos / rope_sin need at least"):
         F.fused_mla(kv, torch.zeros(128, 512, device=cuda), q_rope, W_UV, cos[:10], sin[:10], cfg)
+
+
+# ---------------------------------------------------------------------------
+# C ABI: several query tokens per sequence, head counts that leave padded rows
+# in the 32-row query blocks, absorption inside the call, ragged caches
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("heads,qps,variant", [(48, 1, 2), (48, 3, 2), (16, 2, 2), (128, 2, 2), (48, 3, 1)])
+def test_capi_multi_query_absorb(cuda, heads, qps, variant):
+    import ctypes
+
+    from latent_attn import capi
+
+    lib = capi.load()
+    cfg = cfg_with_heads(heads)
+    d = dims(cfg)
+    lens = [257, 1000, 64]
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(offs[-1])
+    B = len(lens)
+    kv = make_cache((T,), cfg, "bf16", 71 + heads + qps, cuda)
+    W_UK, W_UV = make_weights(cfg, "bf16", 72, cuda)
+    q_nope, q_rope = make_queries((B * qps,), cfg, 73 + qps, cuda)
+    cos, sin = rope(max(lens), cfg, cuda)
+    off_t = torch.tensor(offs, dtype=torch.int32, device=cuda)
+    out = torch.full((B * qps, heads, cfg.v_head_dim), float("nan"), device=cuda)
+    a = capi.DecodeArgs()
+    a.kv_cache, a.kv_dtype, a.total_rows, a.num_seqs = kv.data_ptr(), capi.LA_DTYPE_BF16, T, B
+    a.seq_offsets, a.queries_per_seq = off_t.data_ptr(), qps
+    a.q_nope, a.W_UK, a.w_uk_dtype = q_nope.data_ptr(), W_UK.data_ptr(), capi.LA_DTYPE_BF16
+    a.q_rope, a.W_UV, a.w_uv_dtype = q_rope.data_ptr(), W_UV.data_ptr(), capi.LA_DTYPE_BF16
+    a.rope_cos, a.rope_sin, a.rope_rows = cos.data_ptr(), sin.data_ptr(), cos.shape[0]
+    a.output, a.cfg, a.kernel_variant, a.chunk_rows = out.data_ptr(), capi.config(cfg), variant, 192
+    ws = torch.empty(lib.la_mla_decode_workspace_size(ctypes.byref(a)), dtype=torch.uint8, device=cuda)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    st = lib.la_mla_decode(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == 0, lib.la_status_string(st).decode()
+    torch.cuda.synchronize()
+    kvn, qn, qr, wk, wv = to_np(kv), to_np(q_nope), to_np(q_rope), to_np(W_UK), to_np(W_UV)
+    ref = np.zeros((B * qps, heads, cfg.v_head_dim))
+    for s_ in range(B):
+        for j in range(qps):
+            t = s_ * qps + j
+            qa = mo.absorb_q(qn[t], wk, d)
+            acc, _ = mo.absorbed_latent(kvn[offs[s_]:offs[s_ + 1]], qa, qr[t], to_np(cos), to_np(sin), d)
+            ref[t] = mo.project_wuv(acc, wv, d)
+    assert_close(out.cpu().numpy(), ref, "bf16", f"heads {heads} qps {qps} variant {variant}")
