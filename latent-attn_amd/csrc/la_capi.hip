@@ -159,8 +159,8 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   pl.part_o_off = off;
   off += align_up((size_t)pl.num_slots * p->Hq * c.kv_lora_rank * (pl.mfma ? 2 : 4));
   if (pl.mfma) {
-    pl.part_scale_off = off;
-    off += align_up((size_t)pl.num_slots * p->Hq * sizeof(float));
+    pl.part_scale_off = off;  // two per row (column halves), then part_m: one per row
+    off += align_up((size_t)pl.num_slots * p->Hq * 3 * sizeof(float));
   }
   pl.part_lse_off = off;
   off += align_up((size_t)pl.num_slots * p->Hq * sizeof(float));
@@ -230,6 +230,7 @@ int run(const la_decode_args* a, hipStream_t stream) {
   p.part_o = reinterpret_cast<float*>(ws + plan.part_o_off);
   p.part_lse = reinterpret_cast<float*>(ws + plan.part_lse_off);
   p.part_scale = plan.mfma ? reinterpret_cast<float*>(ws + plan.part_scale_off) : nullptr;
+  p.part_m = plan.mfma ? p.part_scale + (size_t)plan.num_slots * p.Hq * 2 : nullptr;
   if (plan.num_chunks > 0) {
     if (plan.mfma && !plan.absorb_prep) {
       hipError_t e = launch_prep_q(p, stream);

@@ -67,15 +67,23 @@ struct DecodeProblem {
   int chunk_len;
   int num_chunks;
   int num_slots;
-  float* part_o;       // fp32 rows, or fp16 rows when part_f16 (see part_scale)
-  float* part_lse;
-  int part_f16;        // 1: part_o holds fp16 rows O * 2^-e, e chosen per row so |.| < 1
-  float* part_scale;   // part_f16: 2^e per (slot, hq), the factor that restores the row
+  float* part_o;       // fp32 rows O / l, or (part_f16) fp16 rows, see below
+  float* part_lse;     // base-2 log-sum-exp m + log2(l) of the slot's scores
+  // part_f16 (MFMA kernel): part_o row (slot, hq) holds the unnormalised
+  // numerator N = sum_pos 2^(s_pos - m) V_pos as fp16 N * 2^-e, with e chosen
+  // per half row (columns 0..255, 256..511) so every value is below 1;
+  // part_scale[2 row + half] = 2^e and part_m[row] = m. O / l = N / l with
+  // 1 / l = 2^(m - lse).
+  int part_f16;
+  float* part_scale;
+  float* part_m;
 };
 
-// Partial row (slot, hq) element i as fp32.
+// Partial row (slot, hq) element i as fp32 O / l.
 __device__ inline float load_part(const DecodeProblem& p, int64_t row, int i) {
-  if (p.part_f16) return (float)reinterpret_cast<const _Float16*>(p.part_o)[row * p.dc + i] * p.part_scale[row];
+  if (p.part_f16)
+    return (float)reinterpret_cast<const _Float16*>(p.part_o)[row * p.dc + i] * p.part_scale[2 * row + (i >= 256)] *
+           exp2f(p.part_m[row] - p.part_lse[row]);
   return p.part_o[row * p.dc + i];
 }
 

@@ -59,28 +59,37 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kHG = 128;               // heads per group (block)
 constexpr int kCtBytes = kT * kDc * 2;       // 32768: c_t rows, 1024 B each
 constexpr int kRopeOff = kCtBytes;           // k_rope rows, 128 B each
-constexpr int kCosOff = kRopeOff + kT * 128; // cos rows (32 floats)
-constexpr int kSinOff = kCosOff + kT * 128;  // sin rows
-constexpr int kBufBytes = kSinOff + kT * 128;  // 45056
+constexpr int kBufBytes = kRopeOff + kT * 128;  // 36864: one tile
 constexpr int kNBuf = 3;
-constexpr int kScratchOff = kNBuf * kBufBytes;  // per-wave 32 floats
-constexpr int kQropeOff = kScratchOff + kWaves * 32 * 4;  // q rope k-steps: [wave][r][lane] 16 B
-constexpr int kLdsBytes = kQropeOff + kHG * kDr * 2;
+// cos / sin rows (32 floats each) of the tile being staged. They are read
+// only by that tile's RoPE, in the iteration that copies them, so one buffer
+// serves every tile.
+constexpr int kCosOff = kNBuf * kBufBytes;
+constexpr int kSinOff = kCosOff + kT * 128;
+constexpr int kQropeOff = kSinOff + kT * 128;         // q rope k-steps: [wave][r][lane] 16 B
+constexpr int kPtabOff = kQropeOff + kHG * kDr * 2;   // P operands: [parity][wave][ks][lane] 16 B
+constexpr int kPtabPar = kWaves * 2 * 1024;
+constexpr int kAtabWave = 160;                        // per wave: 32 alphas, rescale flag at +128
+constexpr int kAtabOff = kPtabOff + 2 * kPtabPar;     // [parity][wave]
+constexpr int kAtabPar = kWaves * kAtabWave;
+constexpr int kLdsBytes = kAtabOff + 2 * kAtabPar;
 constexpr int kDmaPerWave = 11;        // 8 c_t rows + k_rope + cos + sin
 constexpr int kRescaleSlack = 8;       // log2 units before the running max moves
 constexpr int kQkDepth = 8;            // score A operands read this many k-steps ahead
-constexpr int kPvDepth = 7;            // value reads this many PV steps ahead (2 per step, lgkmcnt <= 15)
-constexpr int kRotStep = 27;           // PV step after which the RoPE reads of tile t+2 are issued
-constexpr int kQrAt = 32 - kQkDepth;   // QK step before which the q_rope table reads are issued
+constexpr int kPvSteps = 16;           // PV operand steps: (ks, column block), 2 MFMAs each
+constexpr int kPvDepth = 6;            // value-read pairs in flight (2 reads per step, lgkmcnt <= 15)
+constexpr int kRotStep = 13;           // PV step after which the RoPE reads of tile t+2 are issued
+constexpr int kQrAt = 32 - kQkDepth;   // QK step before which the q_rope and partner-P reads are issued
 constexpr int kTrAt = 36 - kPvDepth;   // QK steps kTrAt.. issue the first kPvDepth PV value-read pairs
-constexpr int kSmSettle = 1;           // PV step after which softmax(t+1) starts (settle + mask)
-constexpr int kSmExp0 = 8;             // PV steps kSmExp0 .. +15 take one exp2 each
+constexpr int kSmSettle = 1;           // softmax slot (two per PV step) that starts softmax(t+1)
+constexpr int kSmExp0 = 8;             // softmax slots kSmExp0 .. +15 take one exp2 each
 
 // LDS issue order of one iteration (all reads counted by lgkmcnt):
-//   QK:  A(0..D-1); per step kk: [kk == kQrAt: 4 q_rope reads] wait A(kk),
-//        MFMA, A(kk+D), [kk >= kTrAt: value-read pair kk-kTrAt];
-//   PV:  per step s: wait pair s, MFMA, pair s+kPvDepth, [s == kRotStep: 4
-//        RoPE reads].
+//   QK:  [partner flag] A(0..D-1); per step kk: [kk == kQrAt: 4 q_rope
+//        reads, 2 partner-P reads] wait A(kk), MFMA, A(kk+D), [kk >= kTrAt:
+//        value-read pair kk-kTrAt];
+//   PV:  per step s: wait pair s, 2 MFMAs, pair s+kPvDepth, [s == kRotStep:
+//        4 RoPE reads].
 // qk_later(kk) / pv_later(s) = LDS reads issued after the awaited one and
 // before its wait; lgkmcnt(that) then guarantees it has completed.
 constexpr int qk_later(int kk) {
@@ -91,7 +100,7 @@ constexpr int qk_later(int kk) {
     ++seq;
   }
   for (int k = 0; k <= kk; ++k) {
-    if (k == kQrAt) seq += 4;
+    if (k == kQrAt) seq += 6;
     if (k == kk) return seq - seq_a - 1;
     if (k + D < 36) {
       if (k + D == kk) seq_a = seq;
@@ -106,7 +115,7 @@ constexpr int pv_later(int s) {
   int seq = 2 * kPvDepth, seq_s = s < kPvDepth ? 2 * s : -1;
   for (int k = 0; k <= s; ++k) {
     if (k == s) return seq - seq_s - 2;
-    if (k + kPvDepth < 32) {
+    if (k + kPvDepth < kPvSteps) {
       if (k + kPvDepth == s) seq_s = seq;
       seq += 2;
     }
@@ -319,6 +328,24 @@ __device__ inline void wait_lgkm(V& a) {
   asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "n"(N));
 }
 
+template <int N, typename V>
+__device__ inline void wait_lgkm(i16x4& a, i16x4& b, V& c, V& d) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N));
+}
+// Marks v as produced here (no code): for a value read by inline asm whose
+// completion an earlier, later-issued wait already guarantees.
+template <typename V>
+__device__ inline void tie(V& v) {
+  asm volatile("" : "+v"(v));
+}
+__device__ inline float lds_rd32(const lchar* L, uint32_t off) {
+  float r;
+  const uint32_t addr = (uint32_t)(uintptr_t)(L + off);
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+
 // Calls f(std::integral_constant<int, i>) for i = 0 .. N-1.
 template <int I, int N, typename F>
 __device__ inline void static_for_impl(F&& f) {
@@ -370,8 +397,7 @@ __device__ inline void issue_copy(const DecodeProblem& p, const SegCtx& sg, int 
       const uint32_t toff = (uint32_t)(rope_row(p, sg.pos0 + r) * (kDr / 2) * 4 + (lane & 7) * 16);
       const float* tab = J == 9 ? p.rope_cos : p.rope_sin;
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(tab) + toff,
-                                       (lds_void*)(L + buf + (J == 9 ? kCosOff : kSinOff) + r_first * 128), 16, 0,
-                                       0);
+                                       (lds_void*)(L + (J == 9 ? kCosOff : kSinOff) + r_first * 128), 16, 0, 0);
     }
   }
 }
@@ -402,8 +428,8 @@ __device__ inline RotIn rot_issue(const lchar* L, uint32_t buf, int wave, int la
   r.pb = buf + kRopeOff + row * 128 + (((4 + (u >> 1)) ^ f) << 4) + 8 * (u & 1);
   r.ka = lds_rd64(L, r.pa);
   r.kb = lds_rd64(L, r.pb);
-  r.c = lds_rd128<f32x4>(L, buf + kCosOff + row * 128 + 16 * u);
-  r.s = lds_rd128<f32x4>(L, buf + kSinOff + row * 128 + 16 * u);
+  r.c = lds_rd128<f32x4>(L, kCosOff + row * 128 + 16 * u);
+  r.s = lds_rd128<f32x4>(L, kSinOff + row * 128 + 16 * u);
   return r;
 }
 
@@ -458,7 +484,6 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
   block_coords(p.num_chunks, groups, &chunk, &group);
   if (chunk >= p.num_chunks) return;
   const int hg_heads = min(kHG, p.Hq - group * kHG);
-  const uint32_t scratch = kScratchOff + 128 * wave;  // per-wave 32 floats
 
   const int64_t end_all = seq_begin(p, p.num_seqs);
   int64_t lo = (int64_t)chunk * p.chunk_len;
@@ -534,18 +559,40 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     rotate_rows<KT>(L, 0, wave, lane_id());  // fresh lane index: no spilled addresses
 
     // Software pipeline over tiles; iteration t (from -1):
-    //   [apply the O rescale decided by softmax(t)]
+    //   [apply the rescale of own-head O rows decided by softmax(t)]
     //   QK(t+1) -> s_next, with the HBM->LDS copies of tile t+2 riding along;
+    //   [apply the partner's rescale to its O rows held here]
     //   PV(t): O += P(t) . V(t), with softmax(t+1) (s_next -> P(t+1)) spread
-    //   between its MFMAs; then RoPE of tile t+2 (own rows) and a barrier.
+    //   between its MFMAs; then RoPE of tile t+2 (own rows), P(t+1) and the
+    //   rescale of softmax(t+1) published in LDS, and a barrier.
+    // Work split: wave w owns heads 32w.. for QK and the softmax. For PV the
+    // waves pair up (w, w^1): each holds O for the pair's 64 heads over one
+    // half of the latent columns (256 * (w & 1) ..), so it reads half of the
+    // value tile and takes the partner's P(t) from LDS. acc[cb] holds own
+    // heads, acc[8 + cb] the partner's, column block cb of the half.
     // Buffers: tile k lives in buffer k % 3. In iteration t, V(t) and K(t+1)
     // are read and tile t+2 is written; t+2 = t-1 (mod 3) was last read in
-    // iteration t-1, before the barrier that opens iteration t.
+    // iteration t-1, before the barrier that opens iteration t. P and rescale
+    // tables alternate by parity, so a table is rewritten only after the
+    // barrier that follows its last read.
     // Every LDS read that a static lgkmcnt count includes is always issued;
     // where its data is not needed it reads a valid buffer and is dropped.
+    const int ch = wave & 1;   // column half of the PV split
+    const int pw = wave ^ 1;   // partner wave (same heads for PV, other half)
     vec p_cur[2] = {};         // P(t); zero for t = -1
     float alpha_pend = 1.f;    // O rescale owed before PV(t) (per head = lane % 32)
     bool resc_pend = false;    // wave-uniform
+    {
+      // P(-1) = 0 for the partner read of iteration -1; no rescale pending
+      const int lz = lane_id();
+      const vec zero = {};
+#pragma unroll
+      for (int par = 0; par < 2; ++par) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) lds_st(L, kPtabOff + par * kPtabPar + wave * 2048 + ks * 1024 + 16 * lz, zero);
+        if (lz < 40) lds_st(L, kAtabOff + par * kAtabPar + wave * kAtabWave + 4 * lz, 0.f);
+      }
+    }
     for (int t = -1; t < ntiles; ++t) {
       lds_barrier();  // tile t+1 staged and rotated by every wave; iteration t-1 done
       const int lane = lane_id();
@@ -557,24 +604,24 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       const uint32_t cur = ((t < 0 ? 0 : t) % kNBuf) * kBufBytes;  // t = -1: tile 0, with P = 0
       const uint32_t nxt = ((t + 1) % kNBuf) * kBufBytes;
       const uint32_t dbuf = ((t + 2) % kNBuf) * kBufBytes;
+      const int par = t & 1;  // tables of P(t) and of softmax(t)'s rescale
+      const uint32_t atab = kAtabOff + par * kAtabPar;
 
-      // ---- O *= alpha for heads whose running max moved in softmax(t) ----
-      // O rows are heads 8(i/4) + 4*g2 + (i%4); alpha of head h sits in lane h.
+      // ---- own-head O rows *= alpha where softmax(t) moved the running max ----
+      // O rows are heads 8(i/4) + 4*g2 + (i%4); alpha of head h was published
+      // by this wave (lane h) at the end of iteration t-1.
       if (resc_pend) {
-        if (lane < 32) lds_st(L, scratch + 4 * lane, alpha_pend);
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): own LDS write before own read
         settle_acc(acc);
         f32x16 a16;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const f32x4 a4 = lds_ld<f32x4>(L, scratch + 4 * (8 * q + 4 * g2));
+          const f32x4 a4 = lds_ld<f32x4>(L, atab + wave * kAtabWave + 4 * (8 * q + 4 * g2));
 #pragma unroll
           for (int r = 0; r < 4; ++r) a16[4 * q + r] = a4[r];
         }
-        // one 16-register block at a time, pinned back to AGPRs after each,
-        // so the rescale needs 16 temporaries instead of 256
+        // one 16-register block at a time, pinned back to AGPRs after each
 #pragma unroll
-        for (int nb = 0; nb < 16; ++nb) {
+        for (int nb = 0; nb < 8; ++nb) {
           acc[nb] *= a16;
           pin_agpr(acc[nb]);
           __builtin_amdgcn_sched_barrier(0);
@@ -582,19 +629,22 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         acc_ready(acc);
         resc_pend = false;
       }
+      // the partner's flag for the same rescale (applied to its rows before PV)
+      float pflag = lds_rd32(L, atab + pw * kAtabWave + 128);
 
       // ---- QK(t+1): S^T[pos][head] over 36 k-steps (32 latent + 4 rope) ----
       // A operand of k-step kk: tile row arow = lane%32, logical chunk
       // 2kk + g2. For c_t (kk < 32) the byte offset inside the 1024-aligned row
       // is 16((2kk + g2) ^ fc(arow)) = 32kk ^ 16(g2 ^ fc(arow)), so every
       // address is one lane constant XOR an immediate; the same holds for the
-      // 128-B k_rope rows and the q_rope table with fr. A operands are read
-      // kQkDepth k-steps ahead of their MFMA. After the last tile the phase
-      // runs on a valid buffer and its result is dropped.
+      // 128-B k_rope rows with fr. A operands are read kQkDepth k-steps ahead
+      // of their MFMA. After the last tile the phase runs on a valid buffer
+      // and its result is dropped.
       const int arow = lane & 31;
       const uint32_t ct_x = (nxt + arow * 1024) | (16 * (g2 ^ fc(arow)));
       const uint32_t rp_x = (nxt + kRopeOff + arow * 128) | (16 * (g2 ^ fr(arow)));
       const uint32_t qr_x = kQropeOff + 4096 * wave + 16 * lane;
+      const uint32_t pp_x = kPtabOff + par * kPtabPar + pw * 2048 + 16 * lane;
       auto a_off = [&](int kk) -> uint32_t { return kk < 32 ? (ct_x ^ (32 * kk)) : (rp_x ^ (32 * (kk - 32))); };
 
       // PV(t) value reads: lane (q16, s16), read x of step (ks, nb) supplies
@@ -602,23 +652,25 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // + 4(q16>>1) + (s16>>2) (P's k-slot j of lane half g2 is position
       // 16ks + 8(j>>2) + 4g2 + (j&3), the S^T accumulator layout). fc(rho) =
       // 4(s16>>2) + 2x + (q16>>1) is independent of ks and nb, so the address
-      // is base_x ^ 64nb with 16384ks as the immediate offset.
+      // is base_x ^ 64nb with 16384ks as the immediate offset; this wave's
+      // column blocks are nb = 8ch + cb.
       const int lg = 2 * (q16 & 1) + ((s16 & 3) >> 1);
       const uint32_t trow = cur + (4 * (q16 >> 1) + (s16 >> 2)) * 1024;
       const uint32_t zlo = 64 * (s16 >> 2) + 8 * (s16 & 1);
-      const uint32_t tb0 = trow | (zlo + 16 * (lg ^ (q16 >> 1)));
-      const uint32_t tb1 = (trow + 8 * 1024) | (zlo + 16 * (lg ^ (2 + (q16 >> 1))));
+      const uint32_t tb0 = (trow | (zlo + 16 * (lg ^ (q16 >> 1)))) ^ (512 * ch);
+      const uint32_t tb1 = ((trow + 8 * 1024) | (zlo + 16 * (lg ^ (2 + (q16 >> 1))))) ^ (512 * ch);
       TrPair tr[kPvDepth];
       auto b_issue = [&](TrPair& r, auto step_c) {
         constexpr int step = decltype(step_c)::value;
-        constexpr int ks = step >> 4, nb = step & 15;
-        r.x0 = lds_tr<16384 * ks>(L, tb0 ^ (64 * nb));
-        r.x1 = lds_tr<16384 * ks>(L, tb1 ^ (64 * nb));
+        constexpr int ks = step >> 3, cb = step & 7;
+        r.x0 = lds_tr<16384 * ks>(L, tb0 ^ (64 * cb));
+        r.x1 = lds_tr<16384 * ks>(L, tb1 ^ (64 * cb));
       };
 
       f32x16 s_next;
       vec ar[kQkDepth];
       vec qr[4];
+      vec pp[2];  // partner's P(t), read at step kQrAt
       static_for<kQkDepth>([&](auto i) { ar[decltype(i)::value] = lds_rd128<vec>(L, a_off(decltype(i)::value)); });
       static_for<36>([&](auto kk_c) {
         constexpr int kk = decltype(kk_c)::value;
@@ -626,9 +678,12 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         if constexpr (kk == kQrAt) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) qr[r] = lds_rd128<vec>(L, qr_x + 1024 * r);
+          pp[0] = lds_rd128<vec>(L, pp_x);
+          pp[1] = lds_rd128<vec>(L, pp_x + 1024);
         }
         vec& a = ar[kk % D];
         wait_lgkm<qk_later(kk)>(a);
+        if constexpr (kk == 0) tie(pflag);  // issued before A(0), so complete
         if constexpr (kk < 32) {
           if constexpr (kk == 0) O_::mma_v0(s_next, a, qb[kk]);
           else O_::mma_v(s_next, a, qb[kk]);
@@ -692,127 +747,170 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         }
       };
 
-      // ---- PV(t): O[head][c] += P[head][pos] . V[pos][c], 16 column blocks ----
-      // Step s waits for its value reads (count from pv_later: LDS operations
-      // complete in order), runs its MFMA, then issues the reads of step
-      // s + kPvDepth into the freed ring slot. After step kRotStep the four
-      // RoPE reads of tile t+2 go out (always; dropped without a tile).
+
+      // ---- partner-head O rows *= alpha where the partner's softmax(t) moved its max ----
+      if (__builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, pflag)) != 0) {
+        f32x16 a16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 a4 = lds_ld<f32x4>(L, atab + pw * kAtabWave + 4 * (8 * q + 4 * g2));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) a16[4 * q + r] = a4[r];
+        }
+        settle_acc(acc);
+#pragma unroll
+        for (int nb = 8; nb < 16; ++nb) {
+          acc[nb] *= a16;
+          pin_agpr(acc[nb]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        acc_ready(acc);
+      }
+
+      // ---- PV(t): O[head][c] += P[head][pos] . V[pos][c] over the pair's 64 heads ----
+      // Step s = (ks, column block cb) waits for its value reads (count from
+      // pv_later: LDS operations complete in order), runs the own-head and the
+      // partner-head MFMA on them, then issues the reads of step s + kPvDepth
+      // into the freed ring slot. After step kRotStep the four RoPE reads of
+      // tile t+2 go out (always; dropped without a tile). Softmax(t+1) takes
+      // two slots per step.
       operands_ready(p_cur[0], p_cur[1]);
       RotIn rot;
-      static_for<32>([&](auto step_c) {
+      static_for<kPvSteps>([&](auto step_c) {
         constexpr int step = decltype(step_c)::value;
+        constexpr int ks = step >> 3, cb = step & 7;
         TrPair& bc = tr[step % kPvDepth];
-        wait_lgkm<pv_later(step)>(bc.x0, bc.x1);
+        if constexpr (step == 0) wait_lgkm<pv_later(0)>(bc.x0, bc.x1, pp[0], pp[1]);
+        else wait_lgkm<pv_later(step)>(bc.x0, bc.x1);
         i16x8 bv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           bv[e] = bc.x0[e];
           bv[4 + e] = bc.x1[e];
         }
-        O_::mma_a(acc[step & 15], p_cur[step >> 4], __builtin_bit_cast(vec, bv));
-        if constexpr (step + kPvDepth < 32) b_issue(bc, std::integral_constant<int, step + kPvDepth>());
+        const vec bvec = __builtin_bit_cast(vec, bv);
+        O_::mma_a(acc[cb], p_cur[ks], bvec);
+        O_::mma_a(acc[8 + cb], pp[ks], bvec);
+        if constexpr (step + kPvDepth < kPvSteps) b_issue(bc, std::integral_constant<int, step + kPvDepth>());
+        sm_piece(std::integral_constant<int, 2 * step>());
         if constexpr (step == kRotStep) {
           wait_vm<0>();  // this wave's copies of tile t+2 have landed
           rot = rot_issue(L, dbuf, wave, lane);
         }
-        sm_piece(step_c);
+        sm_piece(std::integral_constant<int, 2 * step + 1>());
         __builtin_amdgcn_sched_barrier(0);
       });
       if (do_dma) rot_finish<KT>(L, rot);
       else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(rot.ka), "+v"(rot.kb), "+v"(rot.c), "+v"(rot.s));
+      // ---- publish P(t+1) and softmax(t+1)'s rescale for the partner ----
+      {
+        const int npar = (t + 1) & 1;
+        const uint32_t ptab = kPtabOff + npar * kPtabPar + wave * 2048 + 16 * lane;
+        lds_st(L, ptab, p_next[0]);
+        lds_st(L, ptab + 1024, p_next[1]);
+        const uint32_t natab = kAtabOff + npar * kAtabPar + wave * kAtabWave;
+        if (lane < 32) lds_st(L, natab + 4 * lane, alpha_pend);
+        if (lane == 0) lds_st(L, natab + 128, resc_pend ? 1.f : 0.f);
+      }
       p_cur[0] = p_next[0];
       p_cur[1] = p_next[1];
     }
 
-    // ---- segment end: l over both lane halves; normalise; write the slot ----
+    // ---- segment end: l over both lane halves; write the slot ----
+    // This wave holds the pair's 64 heads (own: acc[0..7], partner:
+    // acc[8..15]) over column half ch. Rows go out unnormalised as fp16
+    // N * 2^-e per half row, 2^(e-1) <= max_c |N[c]| < 2^e (every value below 1
+    // in magnitude, 11 significant bits relative to the half-row max): no
+    // value crosses waves. The softmax owner writes m and m + log2(l).
     settle_acc(acc);
     const int le = lane_id();  // fresh: the prologue's lane index would come back from a spill slot
     const int g2 = le >> 5;
     const float l_tot = sum_halves(l_run);
     const int64_t slot = (int64_t)chunk + s;
-    const int64_t hq0 = slot * p.Hq + group * kHG + 32 * wave;
-    if (le < 32) {
-      lds_st(L, scratch + 4 * le, 1.f / l_tot);
-      if (32 * wave + le < hg_heads) p.part_lse[hq0 + le] = m_run + log2f(l_tot);
+    const int64_t hqg = slot * p.Hq + group * kHG;  // slot row of head 0 of the group
+    if (le < 32 && 32 * wave + le < hg_heads) {
+      p.part_lse[hqg + 32 * wave + le] = m_run + log2f(l_tot);
+      p.part_m[hqg + 32 * wave + le] = m_run;
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    f32x16 il16;
+    // register i of a block: row 8(i/4) + 4*g2 + (i%4), column lane%32 of the block.
+    f32x16 am0 = {}, am1 = {};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4 il = lds_ld<f32x4>(L, scratch + 4 * (8 * q + 4 * g2));
+    for (int cb = 0; cb < 8; ++cb) {
+      const f32x16 a = acc[cb], b = acc[8 + cb];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) il16[4 * q + r] = il[r];
-    }
-    // register i of block nb: head 8(i/4) + 4*g2 + (i%4), column 32nb + lane%32.
-    // Heads come in 16-aligned groups, so validity is uniform per i.
-    // Rows go out as fp16 O * 2^-e with 2^(e-1) <= max_c |O[c]| < 2^e (so
-    // every value is below 1 in magnitude and keeps 11 significant bits
-    // relative to the row max); 2^e goes to part_scale.
-    f32x16 am = {};
-#pragma unroll
-    for (int nb = 0; nb < 16; ++nb) {
-      const f32x16 a = acc[nb];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) am[i] = fmaxf(am[i], fabsf(a[i]));
+      for (int i = 0; i < 16; ++i) {
+        am0[i] = fmaxf(am0[i], fabsf(a[i]));
+        am1[i] = fmaxf(am1[i], fabsf(b[i]));
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
+    f32x16 mul0, mul1;
+    float sc0 = 1.f, sc1 = 1.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) am[i] = max32(am[i]);  // over the 32 lanes (columns) of this half
-    f32x16 mul;
-    float my_scale = 1.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int e = __builtin_amdgcn_frexp_expf(am[i] * il16[i]);  // 0 for a zero row
-      mul[i] = il16[i] * __builtin_amdgcn_ldexpf(1.f, -e);
-      if ((le & 31) == i) my_scale = __builtin_amdgcn_ldexpf(1.f, e);
+    for (int i = 0; i < 16; ++i) {  // max over the 32 lanes (columns) of this half, then the scale
+      const int e0 = __builtin_amdgcn_frexp_expf(max32(am0[i]));  // 0 for a zero row
+      const int e1 = __builtin_amdgcn_frexp_expf(max32(am1[i]));
+      mul0[i] = __builtin_amdgcn_ldexpf(1.f, -e0);
+      mul1[i] = __builtin_amdgcn_ldexpf(1.f, -e1);
+      if ((le & 31) == i) {
+        sc0 = __builtin_amdgcn_ldexpf(1.f, e0);
+        sc1 = __builtin_amdgcn_ldexpf(1.f, e1);
+      }
     }
     if ((le & 31) < 16) {
       const int i = le & 31;
       const int hh = 8 * (i >> 2) + 4 * g2 + (i & 3);
-      if (32 * wave + hh < hg_heads) p.part_scale[hq0 + hh] = my_scale;
+      if (32 * wave + hh < hg_heads) p.part_scale[2 * (hqg + 32 * wave + hh) + ch] = sc0;
+      if (32 * pw + hh < hg_heads) p.part_scale[2 * (hqg + 32 * pw + hh) + ch] = sc1;
     }
     // Write-out through LDS (the tile buffers are idle now): each wave stages
-    // its O^T as fp16 T[column][32 heads] (64-B rows) with 8-B writes of the 4
-    // consecutive heads a lane holds per column, then reads rows of O back with
-    // ds_read_b64_tr_b16 (two reads = 8 columns of one head per lane) and
-    // stores 16 B per lane: 32 stores per lane instead of 256 two-byte ones.
+    // its two 32-head blocks as fp16 T_b[column][32 heads] (64-B rows, 16 KB
+    // each) with 8-B writes of the 4 consecutive heads a lane holds per
+    // column, then reads rows of O back with ds_read_b64_tr_b16 (two reads =
+    // 8 columns of one head per lane) and stores 16 B per lane.
     lds_barrier();  // every wave has finished with the tile buffers
     const uint32_t tbase = 32768 * wave;
 #pragma unroll
-    for (int nb = 0; nb < 16; ++nb) {
-      const f32x16 v = acc[nb] * mul;
+    for (int b = 0; b < 2; ++b) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        i16x4 h4;
+      for (int cb = 0; cb < 8; ++cb) {
+        const f32x16 v = acc[8 * b + cb] * (b == 0 ? mul0 : mul1);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) h4[r] = __builtin_bit_cast(short, (_Float16)v[4 * q + r]);
-        lds_st(L, tbase + (32 * nb + (le & 31)) * 64 + (8 * q + 4 * g2) * 2, h4);
+        for (int q = 0; q < 4; ++q) {
+          i16x4 h4;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) h4[r] = __builtin_bit_cast(short, (_Float16)v[4 * q + r]);
+          lds_st(L, tbase + 16384 * b + (32 * cb + (le & 31)) * 64 + (8 * q + 4 * g2) * 2, h4);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes before its reads
     {
-      // tr read x of round j: lane (q16, s16) supplies T[r0 + s16/4][c0 + 4(s16%4)]
-      // with r0 = 16j + 8(q16>>1) + 4x, c0 = 16(q16&1); lane i of the group gets
-      // T[r0 + v][c0 + i], v = 0..3, i.e. columns r0..r0+3 of head c0 + i.
+      // tr read x of round j (block b = j / 16, jj = j % 16): lane (q16, s16)
+      // supplies T_b[r0 + s16/4][c0 + 4(s16%4)] with r0 = 16jj + 8(q16>>1) + 4x,
+      // c0 = 16(q16&1); lane i of the group gets T_b[r0 + v][c0 + i], v = 0..3,
+      // i.e. columns r0..r0+3 of head c0 + i of the block.
       const int q16 = le >> 4, s16 = le & 15;
-      const int head = 16 * (q16 & 1) + s16;
+      const int hl = 16 * (q16 & 1) + s16;
       const uint32_t rd = tbase + (8 * (q16 >> 1) + (s16 >> 2)) * 64 + (16 * (q16 & 1) + 4 * (s16 & 3)) * 2;
-      _Float16* dsth = reinterpret_cast<_Float16*>(p.part_o) + (hq0 + head) * kDc + 8 * (q16 >> 1);
-      const bool hok = 32 * wave + head < hg_heads;
 #pragma unroll
       for (int j = 0; j < 32; ++j) {
+        const int b = j >> 4, jj = j & 15;
         const i16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)(lds_void*)(L + rd + j * 16 * 64));
+            (__attribute__((address_space(3))) i16x4*)(lds_void*)(L + rd + 16384 * b + jj * 16 * 64));
         const i16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)(lds_void*)(L + rd + j * 16 * 64 + 4 * 64));
+            (__attribute__((address_space(3))) i16x4*)(lds_void*)(L + rd + 16384 * b + jj * 16 * 64 + 4 * 64));
         i16x8 row;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           row[e] = x0[e];
           row[4 + e] = x1[e];
         }
-        if (hok) *reinterpret_cast<i16x8*>(dsth + 16 * j) = row;
+        const int hb = 32 * (b == 0 ? wave : pw) + hl;  // head within the group
+        if (hb < hg_heads)
+          *reinterpret_cast<i16x8*>(reinterpret_cast<_Float16*>(p.part_o) + (hqg + hb) * kDc + 256 * ch + 16 * jj +
+                                    8 * (q16 >> 1)) = row;
       }
     }
     lo = seg_hi;

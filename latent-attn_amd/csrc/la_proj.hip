@@ -278,7 +278,8 @@ struct SlotRow<false> {
   }
 };
 
-// F16: partial rows are fp16 with a per-row power-of-two scale (part_scale).
+// F16: partial rows are fp16 numerators with a power-of-two scale per half row
+// (part_scale) and the running max of their scores (part_m).
 template <bool F16>
 __global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodeProblem p, float* __restrict__ o_merged) {
   typedef typename std::conditional<F16, _Float16, float>::type PT;
@@ -304,25 +305,45 @@ __global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodePro
 #pragma unroll
     for (int u = 0; u < 8; ++u)
       if (u < n) d[u].load(src + (int64_t)u * sstride);
-    // lane i holds slot i of each 64-slot chunk; chunk 0 stays in registers
+    // Lane i holds slot i of each 64-slot chunk (chunk 0 stays in registers).
+    // Denominator weight 2^(lse - M); numerator weight 2^(lse - M) for fp32
+    // O / l rows, 2^(m - M) * 2^e(half) for fp16 numerator rows (lanes 0..31
+    // hold columns 0..255, half 0).
     const float ls0 = lane < n ? lse[(int64_t)lane * p.Hq] : -INFINITY;
-    const float sc0 = F16 && lane < n ? p.part_scale[row0 + (int64_t)lane * p.Hq] : 1.f;
+    float mm0 = 0.f, sa0 = 1.f, sb0 = 1.f;
+    if constexpr (F16) {
+      if (lane < n) {
+        const int64_t pr = row0 + (int64_t)lane * p.Hq;
+        mm0 = p.part_m[pr];
+        sa0 = p.part_scale[2 * pr];
+        sb0 = p.part_scale[2 * pr + 1];
+      }
+    }
     float mx = ls0;
     for (int i = lane + 64; i < n; i += 64) mx = fmaxf(mx, lse[(int64_t)i * p.Hq]);
     mx = wave_max(mx);
     float wsum = 0.f;
     for (int i0 = 0; i0 < n; i0 += 64) {
       const int nb = min(64, n - i0);
-      float wl, sc;
-      if (i0 == 0) {
-        wl = lane < nb ? exp2f(ls0 - mx) : 0.f;
-        sc = sc0;
-      } else {
-        wl = lane < nb ? exp2f(lse[(int64_t)(i0 + lane) * p.Hq] - mx) : 0.f;
-        sc = F16 && lane < nb ? p.part_scale[row0 + (int64_t)(i0 + lane) * p.Hq] : 1.f;
+      float ls = ls0, mm = mm0, sa = sa0, sb = sb0;
+      if (i0 > 0) {
+        const bool ok = lane < nb;
+        const int64_t pr = row0 + (int64_t)(min(i0 + lane, n - 1)) * p.Hq;
+        ls = ok ? lse[(int64_t)(i0 + lane) * p.Hq] : -INFINITY;
+        if constexpr (F16) {
+          mm = ok ? p.part_m[pr] : 0.f;
+          sa = ok ? p.part_scale[2 * pr] : 1.f;
+          sb = ok ? p.part_scale[2 * pr + 1] : 1.f;
+        }
       }
-      wsum += wave_sum(wl);
-      const float wv = wl * sc;  // fp16 rows: the row's power-of-two scale folds into the weight
+      const float wden = lane < nb ? exp2f(ls - mx) : 0.f;
+      wsum += wave_sum(wden);
+      float wlo = wden, whi = wden;
+      if constexpr (F16) {
+        const float a = lane < nb ? exp2f(mm - mx) : 0.f;
+        wlo = a * sa;
+        whi = a * sb;
+      }
       for (int j = 0; j < nb; j += 8) {
         if (i0 > 0 || j > 0) {
 #pragma unroll
@@ -330,8 +351,12 @@ __global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodePro
             if (j + u < nb) d[u].load(src + (int64_t)(i0 + j + u) * sstride);
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (j + u < nb) d[u].fma(__shfl(wv, j + u, 64), o0, o1);
+        for (int u = 0; u < 8; ++u) {
+          if (j + u < nb) {
+            const float w0 = __shfl(wlo, j + u, 64), w1 = __shfl(whi, j + u, 64);
+            d[u].fma(lane < 32 ? w0 : w1, o0, o1);
+          }
+        }
       }
     }
     const float inv = 1.f / wsum;

@@ -203,9 +203,9 @@ def test_zero_query_is_uniform_mean(cuda):
     out = F.fused_mla(kv, q_abs, q_rope, W_UV, cos, sin, cfg).cpu().numpy()
     W = to_np(W_UV).reshape(128, 128, 512)
     # P = 1 exactly for every position, so the only rounding left is the split
-    # partials, stored as fp16 with a power-of-two scale per row (error at most
-    # 2^-12 of the row's max |O| per element): 1e-3 normwise and elementwise
-    # relative to max|ref| -- ten times tighter than the 16-bit contract
+    # partials, stored as fp16 with a power-of-two scale per half row (error at
+    # most 2^-12 of the half row's max |O| per element): 1e-3 normwise and
+    # elementwise relative to max|ref| -- ten times tighter than the 16-bit contract
     ref = W @ to_np(kv)[:, :512].mean(axis=0)
     from oracle.mla_oracle import norm_rel_err
     assert norm_rel_err(out, ref) <= 1e-3, norm_rel_err(out, ref)
