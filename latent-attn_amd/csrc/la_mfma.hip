@@ -165,6 +165,9 @@ struct Ops<__hip_bfloat16> {
   static __device__ inline void mma_a(f32x16& d, vec a, vec b) {
     asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
   }
+  static __device__ inline void mma_a0(f32x16& d, vec a, vec b) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=a"(d) : "v"(a), "v"(b));
+  }
 };
 
 template <>
@@ -182,6 +185,9 @@ struct Ops<__half> {
   }
   static __device__ inline void mma_a(f32x16& d, vec a, vec b) {
     asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
+  }
+  static __device__ inline void mma_a0(f32x16& d, vec a, vec b) {
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=a"(d) : "v"(a), "v"(b));
   }
 };
 
@@ -543,12 +549,15 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     }
 
     float m_run = -INFINITY, l_run = 0.f;
+    // O = 0, written by MFMAs of zero operands straight into the AGPRs (a
+    // zero vector built by the compiler would be kept in a spill slot)
     f32x16 acc[16];
+    {
+      vec z = {}, z2 = {};
+      operands_ready(z, z2);  // VALU-written operands: wait states before the (inline asm) MFMAs
 #pragma unroll
-    for (int nb = 0; nb < 16; ++nb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[nb][e] = 0.f;
-    acc_ready(acc);
+      for (int nb = 0; nb < 16; ++nb) O_::mma_a0(acc[nb], z, z2);
+    }
 
     wait_vm<0>();
     if (!q_head_ok) {
@@ -891,27 +900,38 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // supplies T_b[r0 + s16/4][c0 + 4(s16%4)] with r0 = 16jj + 8(q16>>1) + 4x,
       // c0 = 16(q16&1); lane i of the group gets T_b[r0 + v][c0 + i], v = 0..3,
       // i.e. columns r0..r0+3 of head c0 + i of the block.
-      const int q16 = le >> 4, s16 = le & 15;
+      const int lr = lane_id();  // fresh index: values derived earlier would come back from spill slots
+      const int q16 = lr >> 4, s16 = lr & 15;
       const int hl = 16 * (q16 & 1) + s16;
       const uint32_t rd = tbase + (8 * (q16 >> 1) + (s16 >> 2)) * 64 + (16 * (q16 & 1) + 4 * (s16 & 3)) * 2;
-#pragma unroll
-      for (int j = 0; j < 32; ++j) {
-        const int b = j >> 4, jj = j & 15;
-        const i16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)(lds_void*)(L + rd + 16384 * b + jj * 16 * 64));
-        const i16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)(lds_void*)(L + rd + 16384 * b + jj * 16 * 64 + 4 * 64));
+      _Float16* const obase = reinterpret_cast<_Float16*>(p.part_o) + hqg * kDc + 256 * ch;  // wave-uniform
+      // all 64 reads in flight (each round in its own registers, so no store
+      // source is overwritten while the store may still read it), one wait,
+      // then the 32 stores back to back
+      i16x4 xa[32], xb[32];
+      static_for<32>([&](auto j_c) {
+        constexpr int j = decltype(j_c)::value;
+        constexpr uint32_t off = 16384 * (j >> 4) + (j & 15) * 16 * 64;
+        xa[j] = lds_tr<off>(L, rd);
+        xb[j] = lds_tr<off + 4 * 64>(L, rd);
+      });
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xa[0]), "+v"(xa[1]), "+v"(xa[2]), "+v"(xa[3]), "+v"(xa[4]), "+v"(xa[5]), "+v"(xa[6]), "+v"(xa[7]), "+v"(xb[0]), "+v"(xb[1]), "+v"(xb[2]), "+v"(xb[3]), "+v"(xb[4]), "+v"(xb[5]), "+v"(xb[6]), "+v"(xb[7]));
+      // the waits above cover every read: the rest are ties only
+      asm volatile("" : "+v"(xa[8]), "+v"(xa[9]), "+v"(xa[10]), "+v"(xa[11]), "+v"(xa[12]), "+v"(xa[13]), "+v"(xa[14]), "+v"(xa[15]), "+v"(xb[8]), "+v"(xb[9]), "+v"(xb[10]), "+v"(xb[11]), "+v"(xb[12]), "+v"(xb[13]), "+v"(xb[14]), "+v"(xb[15]));
+      asm volatile("" : "+v"(xa[16]), "+v"(xa[17]), "+v"(xa[18]), "+v"(xa[19]), "+v"(xa[20]), "+v"(xa[21]), "+v"(xa[22]), "+v"(xa[23]), "+v"(xb[16]), "+v"(xb[17]), "+v"(xb[18]), "+v"(xb[19]), "+v"(xb[20]), "+v"(xb[21]), "+v"(xb[22]), "+v"(xb[23]));
+      asm volatile("" : "+v"(xa[24]), "+v"(xa[25]), "+v"(xa[26]), "+v"(xa[27]), "+v"(xa[28]), "+v"(xa[29]), "+v"(xa[30]), "+v"(xa[31]), "+v"(xb[24]), "+v"(xb[25]), "+v"(xb[26]), "+v"(xb[27]), "+v"(xb[28]), "+v"(xb[29]), "+v"(xb[30]), "+v"(xb[31]));
+      static_for<32>([&](auto j_c) {
+        constexpr int j = decltype(j_c)::value;
+        constexpr int b = j >> 4, jj = j & 15;
         i16x8 row;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          row[e] = x0[e];
-          row[4 + e] = x1[e];
+          row[e] = xa[j][e];
+          row[4 + e] = xb[j][e];
         }
         const int hb = 32 * (b == 0 ? wave : pw) + hl;  // head within the group
-        if (hb < hg_heads)
-          *reinterpret_cast<i16x8*>(reinterpret_cast<_Float16*>(p.part_o) + (hqg + hb) * kDc + 256 * ch + 16 * jj +
-                                    8 * (q16 >> 1)) = row;
-      }
+        if (hb < hg_heads) *reinterpret_cast<i16x8*>(obase + (uint32_t)(hb * kDc + 16 * jj + 8 * (q16 >> 1))) = row;
+      });
     }
     lo = seg_hi;
     ++s;

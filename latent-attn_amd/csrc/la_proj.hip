@@ -100,7 +100,17 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
   __shared__ __attribute__((aligned(16))) char wt[128 * kAbsRowBytes];  // dn <= 128 rows
   // q operands (hi, lo) of the 8 k-steps, shared by the 4 waves: [ks][hi|lo][lane] 16 B
   __shared__ __attribute__((aligned(16))) char qs[8 * 2 * 64 * 16];
-  const int h = blockIdx.x, cb = blockIdx.y, t0 = blockIdx.z * 32;
+  // Block id -> (token block tb, head h, column block cb). The q_prep line of
+  // (token, 32-head group, k-step) gathers one 16-B slot from each head of the
+  // group, so the blocks of one (tb, head group, cb) run on one XCD (blocks go
+  // to XCDs round-robin by id % 8) and their slots meet in that XCD's L2
+  // instead of leaving it as partial lines.
+  const int ncb = dc / kAbsCols, nhg = (nh + 31) / 32;
+  const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+  const int grp = x + 8 * (k >> 5);  // (tb, head group, cb) group
+  const int tb = grp / (nhg * ncb), rem = grp - tb * (nhg * ncb);
+  const int h = 32 * (rem / ncb) + (k & 31), cb = rem % ncb, t0 = tb * 32;
+  if (t0 >= tokens || h >= nh) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int nks = NKS > 0 ? NKS : dn / 16;  // <= 8
   if (NKS > 0) dn = 16 * NKS;
@@ -447,7 +457,9 @@ hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype
                               const float* q_rope, float scale, int dR, int tokens, int nh, int dn, int dc, int qps,
                               hipStream_t stream) {
   if (out_mode != 0 && (dc + dR != kQPrepRow || qps <= 0)) return hipErrorInvalidValue;
-  dim3 grid(nh, dc / kAbsCols, (tokens + 31) / 32);
+  // one block per (token block, head, column block), ordered for the XCDs
+  const int64_t groups = (int64_t)((tokens + 31) / 32) * ((nh + 31) / 32) * (dc / kAbsCols);
+  dim3 grid((unsigned)(8 * 32 * ((groups + 7) / 8)));
   const bool d128 = dn == 128;
   if (w_dtype == LA_DTYPE_BF16) {
     auto k = d128 ? absorb_mfma_kernel<__hip_bfloat16, 8> : absorb_mfma_kernel<__hip_bfloat16, 0>;
