@@ -19,12 +19,10 @@
 //          B operand (8 consecutive rows i per lane) comes from
 //          ds_read_b64_tr_b16.
 // combine: merge_slots_kernel, one wave per (query row, weight head), writes
-//          the log-sum-exp merge of the partial slots (fp32, workspace).
-// project: grid (nh, ceil(R/32)), 256 threads. Phase 1 stages the merged O of
-//          32 query tokens of weight head h in LDS (hi/lo 16-bit); phase 2:
-//          wave w owns 32 output columns j, B operand = 16 contiguous bytes of
-//          a W_UV row read straight from global memory (each weight element is
-//          read once per block).
+//          the log-sum-exp merge of the partial slots (fp32, workspace, in the
+//          projection's A-operand order).
+// project: one block per (head, 32-row block, 32 output columns); the 4
+//          waves split the latent dimension and sum their tiles in LDS.
 #include "la_internal.hpp"
 
 #include <type_traits>
@@ -249,8 +247,6 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
 // combine + project
 // ---------------------------------------------------------------------------
 constexpr int kDcP = 512;
-constexpr int kORowBytes = kDcP * 2 + 16;  // 16-bit O row + pad (8 rows -> 8 bank groups)
-constexpr int kProjLdsBytes = 2 * 32 * kORowBytes;
 
 // merge: one wave per (query row r, weight head h). o_merged[r][h][:] =
 // sum_slots 2^(lse_s - m) * part_o_s / sum_slots 2^(lse_s - m), m = max lse
@@ -294,10 +290,14 @@ template <bool F16>
 __global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodeProblem p, float* __restrict__ o_merged) {
   typedef typename std::conditional<F16, _Float16, float>::type PT;
   const int lane = threadIdx.x & 63;
-  const int64_t pair = (int64_t)blockIdx.x * kMergeWaves + (threadIdx.x >> 6);
   const int R = p.num_seqs * p.qps;
-  if (pair >= (int64_t)R * p.nh) return;
-  const int r = (int)(pair / p.nh), h = (int)(pair % p.nh);
+  const int Rp = (R + 31) & ~31;  // rows padded to the projection's 32-row blocks
+  // wave -> (weight head h, query row r), r fastest: the waves of a block write
+  // neighbouring rows, which share the 128-B lines of the operand-order output
+  const int64_t pair = (int64_t)blockIdx.x * kMergeWaves + (threadIdx.x >> 6);
+  if (pair >= (int64_t)Rp * p.nh) return;
+  const int h = (int)(pair / Rp), r = (int)(pair % Rp);
+  if (r >= R) return;
   const int s = r / p.qps;
   const int hq = (r % p.qps) * p.nh + h;
   f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
@@ -373,76 +373,77 @@ __global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodePro
     o0 *= inv;
     o1 *= inv;
   }
-  float* dst = o_merged + ((int64_t)r * p.nh + h) * kDcP + 8 * lane;
+  // o_merged in the projection's A-operand order: block (h, r / 32), k-step
+  // ks = lane / 2 (16 columns), lane slot (r % 32) + 32 (lane % 2): 8 floats.
+  float* dst = o_merged + (((int64_t)h * (Rp / 32) + r / 32) * (kDcP / 16) + (lane >> 1)) * 512 +
+               ((r & 31) + 32 * (lane & 1)) * 8;
   *reinterpret_cast<f32x4*>(dst) = o0;
   *reinterpret_cast<f32x4*>(dst + 4) = o1;
 }
 
-// project: grid (nh, ceil(R/32)), 256 threads. Phase 1 stages the merged O of
-// 32 query rows of weight head h into LDS (16-bit hi/lo); phase 2: wave w owns
-// 32 output columns j, B operand = 16 contiguous bytes of a W_UV row read
-// straight from global memory (each weight element is read once per block).
+// project: one block per (weight head h, 32-row block rb, 32 output columns
+// dq), XCD-ordered so the 4 column blocks of (h, rb) share an L2. Wave w takes
+// the latent columns 128w .. 128w+127 (8 k-steps): A = merged O rows (fp32 in
+// the operand order the merge wrote, split into 16-bit hi/lo), B = 16
+// contiguous bytes of a W_UV row; the 4 partial 32x32 tiles are summed in LDS.
+// Every wave issues its 24 loads at once.
 template <typename WT>
 __global__ __launch_bounds__(256) void project_mfma_kernel(DecodeProblem p, const float* __restrict__ o_merged) {
   typedef Mma<WT> M;
   typedef typename M::vec vec;
-  extern __shared__ __attribute__((aligned(16))) char o_lds[];  // kProjLdsBytes
-  char* o_hi = o_lds;
-  char* o_lo = o_lds + 32 * kORowBytes;
-  const int h = blockIdx.x, r0 = blockIdx.y * 32;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  __shared__ __attribute__((aligned(16))) float red[3][16][64];  // partial tiles of waves 1..3
   const int R = p.num_seqs * p.qps;
+  const int nrb = (R + 31) / 32;
+  const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+  const int grp = x + 8 * (k >> 2);  // (h, rb)
+  const int dq = k & 3;
+  if (grp >= p.nh * nrb) return;
+  const int h = grp / nrb, rb = grp % nrb;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
-  // All global loads first: this wave's 8 rows of merged O (rows past R read
-  // row R-1 and are zeroed) and its 32 W_UV operand vectors.
-  f32x4 oa[8], ob[8];
+  const float* oa = o_merged + (((int64_t)h * nrb + rb) * (kDcP / 16) + 8 * wave) * 512 + 8 * lane;
+  f32x4 olo[8], ohi[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int r = min(r0 + wave + 4 * k, R - 1);
-    const float* src = o_merged + ((int64_t)r * p.nh + h) * kDcP + 8 * lane;
-    oa[k] = *reinterpret_cast<const f32x4*>(src);
-    ob[k] = *reinterpret_cast<const f32x4*>(src + 4);
+  for (int ks = 0; ks < 8; ++ks) {
+    olo[ks] = *reinterpret_cast<const f32x4*>(oa + 512 * ks);
+    ohi[ks] = *reinterpret_cast<const f32x4*>(oa + 512 * ks + 4);
   }
-  const WT* wrow = reinterpret_cast<const WT*>(p.W_UV) + ((int64_t)h * p.dv + 32 * wave + (lane & 31)) * kDcP +
-                   8 * (lane >> 5);
-  vec bw[kDcP / 16];
+  const WT* wrow = reinterpret_cast<const WT*>(p.W_UV) + ((int64_t)h * p.dv + 32 * dq + (lane & 31)) * kDcP +
+                   128 * wave + 8 * (lane >> 5);
+  vec bw[8];
 #pragma unroll
-  for (int ks = 0; ks < kDcP / 16; ++ks) bw[ks] = __builtin_bit_cast(vec, *reinterpret_cast<const i16x8*>(wrow + 16 * ks));
+  for (int ks = 0; ks < 8; ++ks) bw[ks] = __builtin_bit_cast(vec, *reinterpret_cast<const i16x8*>(wrow + 16 * ks));
 
-  // ---- phase 1: merged O of 32 rows -> LDS (hi/lo) ----
+  // out[row][32dq + n], partial over this wave's latent quarter
+  f32x16 acc_hi = {}, acc_lo = {};
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int rr = wave + 4 * k;
-    const bool ok = r0 + rr < R;
+  for (int ks = 0; ks < 8; ++ks) {
     float o[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      o[e] = ok ? oa[k][e] : 0.f;
-      o[4 + e] = ok ? ob[k][e] : 0.f;
+      o[e] = olo[ks][e];
+      o[4 + e] = ohi[ks][e];
     }
     vec vh, vl;
     split8<WT>(o, vh, vl);
-    *reinterpret_cast<vec*>(o_hi + rr * kORowBytes + lane * 16) = vh;
-    *reinterpret_cast<vec*>(o_lo + rr * kORowBytes + lane * 16) = vl;
+    acc_hi = M::mma(vh, bw[ks], acc_hi);
+    acc_lo = M::mma(vl, bw[ks], acc_lo);
+  }
+  f32x16 part;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) part[i] = acc_hi[i] + acc_lo[i] * (1.f / M::kLoScale);
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) red[wave - 1][i][lane] = part[i];
   }
   __syncthreads();
-
-  // ---- phase 2: out[token][32w + n] = sum_c O[token][c] * W_UV[h*dv + 32w + n][c] ----
-  const char* ah = o_hi + (lane & 31) * kORowBytes + 16 * (lane >> 5);
-  const char* al = o_lo + (lane & 31) * kORowBytes + 16 * (lane >> 5);
-  f32x16 acc_hi = {}, acc_lo = {};
+  if (wave == 0) {
 #pragma unroll
-  for (int ks = 0; ks < kDcP / 16; ++ks) {
-    const vec a1 = *reinterpret_cast<const vec*>(ah + 32 * ks);
-    const vec a2 = *reinterpret_cast<const vec*>(al + 32 * ks);
-    acc_hi = M::mma(a1, bw[ks], acc_hi);
-    acc_lo = M::mma(a2, bw[ks], acc_lo);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int m = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-    const int r = r0 + m;
-    if (r < R) p.out[((int64_t)r * p.nh + h) * p.dv + 32 * wave + (lane & 31)] = acc_hi[i] + acc_lo[i] * (1.f / M::kLoScale);
+    for (int i = 0; i < 16; ++i) {
+      const float v = part[i] + red[0][i][lane] + red[1][i][lane] + red[2][i][lane];
+      const int r = 32 * rb + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+      if (r < R) p.out[((int64_t)r * p.nh + h) * p.dv + 32 * dq + (lane & 31)] = v;
+    }
   }
 }
 
@@ -480,26 +481,20 @@ bool project_mfma_supported(const DecodeProblem& p) {
 
 template <typename WT>
 hipError_t launch_proj(const DecodeProblem& p, const float* o_merged, hipStream_t stream) {
-  static bool attr_set = false;  // per instance; setting it twice is harmless
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&project_mfma_kernel<WT>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kProjLdsBytes);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
-  const int R = p.num_seqs * p.qps;
-  dim3 grid(p.nh, (R + 31) / 32);
-  hipLaunchKernelGGL(project_mfma_kernel<WT>, grid, dim3(256), kProjLdsBytes, stream, p, o_merged);
+  const int64_t groups = (int64_t)p.nh * ((p.num_seqs * p.qps + 31) / 32);  // (h, rb)
+  dim3 grid((unsigned)(8 * 4 * ((groups + 7) / 8)));
+  hipLaunchKernelGGL(project_mfma_kernel<WT>, grid, dim3(256), 0, stream, p, o_merged);
   return hipGetLastError();
 }
 
 size_t combine_project_mfma_workspace(const DecodeProblem& p) {
-  return (size_t)p.num_seqs * p.qps * p.nh * kDcP * sizeof(float);
+  const size_t rows = ((size_t)p.num_seqs * p.qps + 31) / 32 * 32;
+  return rows * p.nh * kDcP * sizeof(float);
 }
 
 hipError_t launch_combine_project_mfma(const DecodeProblem& p, float* o_merged, hipStream_t stream) {
-  const int64_t pairs = (int64_t)p.num_seqs * p.qps * p.nh;
-  if (pairs == 0) return hipSuccess;
+  const int64_t pairs = (int64_t)((p.num_seqs * p.qps + 31) / 32 * 32) * p.nh;  // rows padded to 32
+  if (p.num_seqs * p.qps == 0) return hipSuccess;
   const dim3 grid((unsigned)((pairs + kMergeWaves - 1) / kMergeWaves));
   if (p.part_f16)
     hipLaunchKernelGGL((merge_slots_kernel<true>), grid, dim3(kMergeWaves * 64), 0, stream, p, o_merged);
