@@ -281,7 +281,10 @@ __device__ inline float max32(float x) {
 }
 
 // LDS is addressed with 32-bit byte offsets from the start of the dynamic LDS
-// block (address-space-3 pointers), never with 64-bit generic pointers.
+// block (address-space-3 pointers), never with 64-bit generic pointers. The
+// decode kernel declares no static LDS, so its dynamic block starts at LDS
+// address 0 and the inline-asm accessors below use the offset itself as the
+// address (the launcher checks the kernel's static LDS size is 0).
 typedef __attribute__((address_space(3))) char lchar;
 
 template <typename T>
@@ -300,8 +303,7 @@ template <int OFF>
 __device__ inline i16x4 lds_tr(const lchar* L, uint32_t off) {
   static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
   i16x4 r;
-  const uint32_t addr = (uint32_t)(uintptr_t)(L + off);
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(off), "n"(OFF));
   return r;
 }
 
@@ -309,15 +311,13 @@ __device__ inline i16x4 lds_tr(const lchar* L, uint32_t off) {
 template <typename V>
 __device__ inline V lds_rd128(const lchar* L, uint32_t off) {
   V r;
-  const uint32_t addr = (uint32_t)(uintptr_t)(L + off);
-  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(off));
   return r;
 }
 
 __device__ inline i16x4 lds_rd64(const lchar* L, uint32_t off) {
   i16x4 r;
-  const uint32_t addr = (uint32_t)(uintptr_t)(L + off);
-  asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(addr));
+  asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(off));
   return r;
 }
 
@@ -347,8 +347,7 @@ __device__ inline void tie(V& v) {
 }
 __device__ inline float lds_rd32(const lchar* L, uint32_t off) {
   float r;
-  const uint32_t addr = (uint32_t)(uintptr_t)(L + off);
-  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr));
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(off));
   return r;
 }
 
@@ -716,8 +715,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       const int valid = min(kT, seg_len - (t + 1) * kT);
       float m4[4];
       float lmax = -INFINITY;
-      vec p_next[2] = {};
+      uint32_t pw_next[8];  // P(t+1) as bf16/fp16 pairs: word j = positions 2j, 2j+1 of the lane's 16
       float lpart[4] = {0.f, 0.f, 0.f, 0.f};
+      float x_even = 0.f;
       auto sm_piece = [&](auto step_c) {
         constexpr int step = decltype(step_c)::value;
         if constexpr (step == kSmSettle) {
@@ -747,10 +747,23 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           }
         } else if constexpr (step >= kSmExp0 && step < kSmExp0 + 16) {
           // P = 2^(s - m) <= 2^kRescaleSlack; masked and far-below-max scores give 0
+          // The empty asm statements hold each exp and each finished pair of
+          // P in this slot: without them the compiler sinks the whole exp
+          // chain past the PV loop (its only uses are after it), where no
+          // MFMA hides it. l sums the fp32 exps; PV uses them rounded to E
+          // (unbiased rounding, relative error <= 2^-9 per term).
           constexpr int i = step - kSmExp0;
-          const E pe = (E)__builtin_amdgcn_exp2f(s_next[i] - m_run);
-          p_next[i >> 3][i & 7] = pe;
-          lpart[i & 3] += (float)pe;
+          float x = __builtin_amdgcn_exp2f(s_next[i] - m_run);
+          lpart[i & 3] += x;
+          asm volatile("" : "+v"(x), "+v"(lpart[i & 3]));
+          if constexpr ((i & 1) == 0) {
+            x_even = x;
+          } else {
+            typedef E E2 __attribute__((ext_vector_type(2)));
+            const E2 pr = {(E)x_even, (E)x};
+            pw_next[i >> 1] = __builtin_bit_cast(uint32_t, pr);
+            asm volatile("" : "+v"(pw_next[i >> 1]));
+          }
         } else if constexpr (step == kSmExp0 + 16) {
           if (sm) l_run += (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
         }
@@ -815,14 +828,15 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       {
         const int npar = (t + 1) & 1;
         const uint32_t ptab = kPtabOff + npar * kPtabPar + wave * 2048 + 16 * lane;
-        lds_st(L, ptab, p_next[0]);
-        lds_st(L, ptab + 1024, p_next[1]);
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        p_cur[0] = __builtin_bit_cast(vec, u32x4{pw_next[0], pw_next[1], pw_next[2], pw_next[3]});
+        p_cur[1] = __builtin_bit_cast(vec, u32x4{pw_next[4], pw_next[5], pw_next[6], pw_next[7]});
+        lds_st(L, ptab, p_cur[0]);
+        lds_st(L, ptab + 1024, p_cur[1]);
         const uint32_t natab = kAtabOff + npar * kAtabPar + wave * kAtabWave;
         if (lane < 32) lds_st(L, natab + 4 * lane, alpha_pend);
         if (lane == 0) lds_st(L, natab + 128, resc_pend ? 1.f : 0.f);
       }
-      p_cur[0] = p_next[0];
-      p_cur[1] = p_next[1];
     }
 
     // ---- segment end: l over both lane halves; write the slot ----
@@ -969,8 +983,12 @@ template <typename KT>
 hipError_t launch_t(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
   static bool attr_set = false;  // per instance; setting it twice is harmless
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_mfma_kernel<KT>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<KT>);
+    hipFuncAttributes fa;
+    hipError_t e = hipFuncGetAttributes(&fa, fn);
+    if (e != hipSuccess) return e;
+    if (fa.sharedSizeBytes != 0) return hipErrorInvalidKernelFile;  // LDS offsets would not be addresses
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
