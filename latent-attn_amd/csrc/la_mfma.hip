@@ -716,7 +716,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       float m4[4];
       float lmax = -INFINITY;
       uint32_t pw_next[8];  // P(t+1) as bf16/fp16 pairs: word j = positions 2j, 2j+1 of the lane's 16
-      float lpart[4] = {0.f, 0.f, 0.f, 0.f};
+      float lpart[4];
       float x_even = 0.f;
       auto sm_piece = [&](auto step_c) {
         constexpr int step = decltype(step_c)::value;
@@ -754,7 +754,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           // (unbiased rounding, relative error <= 2^-9 per term).
           constexpr int i = step - kSmExp0;
           float x = __builtin_amdgcn_exp2f(s_next[i] - m_run);
-          lpart[i & 3] += x;
+          if constexpr (i < 4) lpart[i] = x;
+          else lpart[i & 3] += x;
           asm volatile("" : "+v"(x), "+v"(lpart[i & 3]));
           if constexpr ((i & 1) == 0) {
             x_even = x;
@@ -811,10 +812,16 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           bv[4 + e] = bc.x1[e];
         }
         const vec bvec = __builtin_bit_cast(vec, bv);
+        // A wave issues in order and an MFMA waits for the previous one to
+        // leave the pipe, so VALU work placed between the two MFMAs runs while
+        // the first executes; placed after both it would wait for the second
+        // to issue.
         O_::mma_a(acc[cb], p_cur[ks], bvec);
+        __builtin_amdgcn_sched_barrier(0);
+        sm_piece(std::integral_constant<int, 2 * step>());
+        __builtin_amdgcn_sched_barrier(0);
         O_::mma_a(acc[8 + cb], pp[ks], bvec);
         if constexpr (step + kPvDepth < kPvSteps) b_issue(bc, std::integral_constant<int, step + kPvDepth>());
-        sm_piece(std::integral_constant<int, 2 * step>());
         if constexpr (step == kRotStep) {
           wait_vm<0>();  // this wave's copies of tile t+2 have landed
           rot = rot_issue(L, dbuf, wave, lane);
