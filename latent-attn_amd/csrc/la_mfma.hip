@@ -19,11 +19,12 @@
 //   * Staging: per tile, wave w copies rows 8w..8w+7 HBM->LDS with
 //     global_load_lds_dwordx4 (c_t rows, k_rope rows, cos and sin rows: 11
 //     copies per wave, no VGPR staging) into a 3-deep ring, two tiles ahead.
-//     Inside a c_t row the 16-B chunk j lives at chunk j ^ fc(row),
-//     fc(row) = 4(row&3) | ((row>>2)&3); inside a k_rope row at j ^ fr(row),
-//     fr(row) = (row>>1)&7. With 64 banks of 4 B this makes both the score
-//     reads (16 rows at one column per 16 lanes) and the transposed value
-//     reads (4 rows x 4 columns per 16 lanes) conflict-free.
+//     c_t row r sits at ct_row_off(r) = 1088r + 16((r/4)%4), unswizzled (one
+//     lane offset serves every row copy); inside a k_rope row the
+//     16-B chunk j lives at j ^ fr(row), fr(row) = (row>>1)&7. With 64 banks
+//     of 4 B both the score reads (16 rows at one column per 16 lanes) and the
+//     transposed value reads (4 rows x 4 columns per 16 lanes) are
+//     conflict-free, and c_t reads need no per-read address arithmetic.
 //     Each wave rotates (RoPE) the k_rope rows it copied itself, so only its
 //     own vmcnt has to drain; one s_barrier per tile publishes the tile.
 //   * Scores: S^T[32 pos x 32 heads] = sum over 36 k-steps of
@@ -57,9 +58,21 @@ constexpr int kT = 32;                 // positions per tile
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kHG = 128;               // heads per group (block)
-constexpr int kCtBytes = kT * kDc * 2;       // 32768: c_t rows, 1024 B each
-constexpr int kRopeOff = kCtBytes;           // k_rope rows, 128 B each
-constexpr int kBufBytes = kRopeOff + kT * 128;  // 36864: one tile
+// c_t row r of a tile starts at LDS byte ct_row_off(r) of its buffer: pitch
+// 1088 B (64 B past a multiple of 256) plus 16 ((r/4) % 4) B, i.e. in 16-B
+// bank slots row r starts at slot 4(r%4) + (r/4)%4 (mod 16), a rotation that
+// spreads the rows without overlapping them. Every read of a tile (score A
+// operands: 16 rows at one chunk per 16 lanes; value reads: 4 consecutive
+// rows x 32 B per 16 lanes, x 64 B per 32) then hits distinct banks, and
+// every address is a lane base plus an instruction immediate.
+constexpr int kRowPitch = 1088;
+__host__ __device__ constexpr int ct_row_off(int r) { return r * kRowPitch + 16 * ((r >> 2) & 3); }
+constexpr int kCtBytes = ct_row_off(kT - 1) + kDc * 2;  // 34800
+// k_rope rows, 128 B each; 128-aligned (as is every buffer) because their
+// swizzled addresses are built with OR / XOR on the low 7 bits
+constexpr int kRopeOff = (kCtBytes + 127) / 128 * 128;  // 34816
+constexpr int kBufBytes = kRopeOff + kT * 128;          // 38912: one tile
+static_assert(kRopeOff % 128 == 0 && kBufBytes % 128 == 0, "k_rope rows must be 128-aligned");
 constexpr int kNBuf = 3;
 // cos / sin rows (32 floats each) of the tile being staged. They are read
 // only by that tile's RoPE, in the iteration that copies them, so one buffer
@@ -223,9 +236,8 @@ __device__ inline void acc_ready(f32x16 (&acc)[16]) {
                "+a"(acc[13]), "+a"(acc[14]), "+a"(acc[15]));
 }
 
-// Chunk swizzles of c_t rows (64 chunks of 16 B) and of 128-B rows (k_rope,
-// the q_rope table): logical chunk j is stored at chunk j ^ f(row).
-__device__ inline int fc(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
+// Chunk swizzle of 128-B rows (k_rope): logical chunk j is stored at chunk
+// j ^ fr(row).
 __device__ inline int fr(int row) { return (row >> 1) & 7; }
 
 // vmcnt(n) with the other counters left alone (gfx9 encoding, n < 16).
@@ -308,10 +320,11 @@ __device__ inline i16x4 lds_tr(const lchar* L, uint32_t off) {
 }
 
 // ds_read_b128 as inline asm, for the same reason; same contract as lds_tr.
-template <typename V>
+template <typename V, int OFF = 0>
 __device__ inline V lds_rd128(const lchar* L, uint32_t off) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
   V r;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(off));
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(off), "n"(OFF));
   return r;
 }
 
@@ -368,49 +381,65 @@ struct TrPair {
   i16x4 x0, x1;
 };
 
+constexpr int kRowBytes = (kDc + kDr) * 2;  // 1152: one packed cache row
+
 struct SegCtx {
   const char* base;  // first byte of the segment's first row
   int64_t pos0;      // in-sequence position of the segment's first row
   int last;          // index of the segment's last row, relative to its first
 };
 
+// Wave w's copies of tile k, rows tb = 32k + 8w ..: per-lane byte offset of
+// row tb's chunk lane (from the segment base), how far the segment's last row
+// is past tb (rows past it re-read the last row: their scores are masked),
+// and the k_rope copy's offset (row min(tb + lane/8, last), the logical
+// chunk (lane%8) ^ fr(row) that lands in chunk lane%8). Offsets stay below
+// 2^32 (segments are capped at kMaxChunkRows rows).
+struct TileDma {
+  uint32_t ct, rope;
+  int dlast;  // last - tb, wave-uniform
+};
+__device__ inline TileDma tile_dma(const SegCtx& sg, int k, int wave, int lane) {
+  const int tb = k * kT + 8 * wave;
+  const int rr = lane >> 3;
+  TileDma d;
+  d.ct = (uint32_t)tb * kRowBytes + 16 * lane;
+  d.dlast = sg.last - tb;
+  d.rope = (uint32_t)min(tb + rr, sg.last) * kRowBytes + kDc * 2 + 16 * ((lane & 7) ^ fr(8 * wave + rr));
+  return d;
+}
+
 // Wave w's HBM->LDS copy J (0..10) of tile k into the buffer at LDS offset
 // buf: J < 8 is the c_t row 8w+J, J = 8 the k_rope rows 8w..8w+7, J = 9 / 10
-// their cos / sin rows. Lane i writes LDS chunk i and fetches the logical
-// chunk that belongs there (i ^ swizzle). Global addresses are a wave-uniform
-// base plus a 32-bit lane offset (segments are capped at kMaxChunkRows rows,
-// tables at 2^24 rows). Rows past the segment end re-read its last row; their
-// scores are masked.
+// their cos / sin rows. Lane i writes LDS chunk i (M0 + 16i): c_t rows land
+// unswizzled at ct_row_off, so the lane offset is the same for every row. The
+// instruction's immediate offset would move the LDS destination too, so row
+// steps go into the VGPR offset.
 template <int J>
 __device__ inline void issue_copy(const DecodeProblem& p, const SegCtx& sg, int k, lchar* L, uint32_t buf, int wave,
-                                  int lane) {
+                                  int lane, const TileDma& d) {
   const int r_first = 8 * wave;
   if constexpr (J < 8) {
-    const int row = r_first + J;
-    const int r = min(k * kT + row, sg.last);
-    const int j = lane ^ fc(row);
-    __builtin_amdgcn_global_load_lds(sg.base + (uint32_t)(r * (kDc + kDr) * 2 + j * 16),
-                                     (lds_void*)(L + buf + row * 1024), 16, 0, 0);
+    const int j = min(J, d.dlast);
+    __builtin_amdgcn_global_load_lds(sg.base + (d.ct + (uint32_t)(j * kRowBytes)),
+                                     (lds_void*)(L + buf + ct_row_off(r_first + J)), 16, 0, 0);
+  } else if constexpr (J == 8) {
+    __builtin_amdgcn_global_load_lds(sg.base + d.rope, (lds_void*)(L + buf + kRopeOff + r_first * 128), 16, 0, 0);
   } else {
     const int row = r_first + (lane >> 3);
     const int r = min(k * kT + row, sg.last);
-    if constexpr (J == 8) {
-      const int jr = (lane & 7) ^ fr(row);
-      __builtin_amdgcn_global_load_lds(sg.base + (uint32_t)(r * (kDc + kDr) * 2 + kDc * 2 + jr * 16),
-                                       (lds_void*)(L + buf + kRopeOff + r_first * 128), 16, 0, 0);
-    } else {
-      const uint32_t toff = (uint32_t)(rope_row(p, sg.pos0 + r) * (kDr / 2) * 4 + (lane & 7) * 16);
-      const float* tab = J == 9 ? p.rope_cos : p.rope_sin;
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(tab) + toff,
-                                       (lds_void*)(L + (J == 9 ? kCosOff : kSinOff) + r_first * 128), 16, 0, 0);
-    }
+    const uint32_t toff = (uint32_t)(rope_row(p, sg.pos0 + r) * (kDr / 2) * 4 + (lane & 7) * 16);
+    const float* tab = J == 9 ? p.rope_cos : p.rope_sin;
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(tab) + toff,
+                                     (lds_void*)(L + (J == 9 ? kCosOff : kSinOff) + r_first * 128), 16, 0, 0);
   }
 }
 
 // All kDmaPerWave copies of tile k.
 __device__ inline void issue_tile_dma(const DecodeProblem& p, const SegCtx& sg, int k, lchar* L, uint32_t buf,
                                       int wave, int lane) {
-  static_for<kDmaPerWave>([&](auto j) { issue_copy<decltype(j)::value>(p, sg, k, L, buf, wave, lane); });
+  const TileDma d = tile_dma(sg, k, wave, lane);
+  static_for<kDmaPerWave>([&](auto j) { issue_copy<decltype(j)::value>(p, sg, k, L, buf, wave, lane, d); });
 }
 
 // Rotate-half RoPE of rows 8w..8w+7 of the tile at LDS offset buf, in place
@@ -505,7 +534,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     }
     const int64_t seg_hi = min(hi, s_hi);
     SegCtx sg;
-    sg.base = reinterpret_cast<const char*>(p.kv) + lo * (kDc + kDr) * 2;
+    sg.base = reinterpret_cast<const char*>(p.kv) + lo * kRowBytes;
     sg.pos0 = lo - s_lo;
     sg.last = (int)(seg_hi - lo - 1);
     const int seg_len = sg.last + 1;
@@ -608,7 +637,6 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       const int q16 = lane >> 4, s16 = lane & 15;
       const int head = 32 * wave + (lane & 31);
       const bool sm = t + 1 < ntiles;  // softmax(t+1) runs in this iteration
-      const bool do_dma = t + 2 < ntiles;  // tile t+2: copies and RoPE
       const uint32_t cur = ((t < 0 ? 0 : t) % kNBuf) * kBufBytes;  // t = -1: tile 0, with P = 0
       const uint32_t nxt = ((t + 1) % kNBuf) * kBufBytes;
       const uint32_t dbuf = ((t + 2) % kNBuf) * kBufBytes;
@@ -642,44 +670,47 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
 
       // ---- QK(t+1): S^T[pos][head] over 36 k-steps (32 latent + 4 rope) ----
       // A operand of k-step kk: tile row arow = lane%32, logical chunk
-      // 2kk + g2. For c_t (kk < 32) the byte offset inside the 1024-aligned row
-      // is 16((2kk + g2) ^ fc(arow)) = 32kk ^ 16(g2 ^ fc(arow)), so every
-      // address is one lane constant XOR an immediate; the same holds for the
-      // 128-B k_rope rows with fr. A operands are read kQkDepth k-steps ahead
-      // of their MFMA. After the last tile the phase runs on a valid buffer
-      // and its result is dropped.
+      // 2kk + g2. For c_t (kk < 32) that is byte ct_row_off(arow) + 16 g2 +
+      // 32kk: a lane base plus the immediate 32kk. For the 128-B k_rope rows
+      // the byte offset is 16((2(kk-32) + g2) ^ fr(arow)) = 32(kk-32) ^
+      // 16(g2 ^ fr(arow)): a lane constant XOR an immediate. A operands are
+      // read kQkDepth k-steps ahead of their MFMA. After the last tile the
+      // phase runs on a valid buffer and its result is dropped.
       const int arow = lane & 31;
-      const uint32_t ct_x = (nxt + arow * 1024) | (16 * (g2 ^ fc(arow)));
+      const uint32_t ct_x = nxt + ct_row_off(arow) + 16 * g2;
       const uint32_t rp_x = (nxt + kRopeOff + arow * 128) | (16 * (g2 ^ fr(arow)));
       const uint32_t qr_x = kQropeOff + 4096 * wave + 16 * lane;
       const uint32_t pp_x = kPtabOff + par * kPtabPar + pw * 2048 + 16 * lane;
-      auto a_off = [&](int kk) -> uint32_t { return kk < 32 ? (ct_x ^ (32 * kk)) : (rp_x ^ (32 * (kk - 32))); };
+      const TileDma dm = tile_dma(sg, t + 2, wave, lane);
+      auto a_rd = [&](auto kk_c) -> vec {
+        constexpr int kk = decltype(kk_c)::value;
+        if constexpr (kk < 32) return lds_rd128<vec, 32 * kk>(L, ct_x);
+        else return lds_rd128<vec>(L, rp_x ^ (32 * (kk - 32)));
+      };
 
       // PV(t) value reads: lane (q16, s16), read x of step (ks, nb) supplies
       // the address of tile[rho][32nb + 16(q16&1) + 4(s16&3)], rho = 16ks + 8x
       // + 4(q16>>1) + (s16>>2) (P's k-slot j of lane half g2 is position
-      // 16ks + 8(j>>2) + 4g2 + (j&3), the S^T accumulator layout). fc(rho) =
-      // 4(s16>>2) + 2x + (q16>>1) is independent of ks and nb, so the address
-      // is base_x ^ 64nb with 16384ks as the immediate offset; this wave's
-      // column blocks are nb = 8ch + cb.
-      const int lg = 2 * (q16 & 1) + ((s16 & 3) >> 1);
-      const uint32_t trow = cur + (4 * (q16 >> 1) + (s16 >> 2)) * 1024;
-      const uint32_t zlo = 64 * (s16 >> 2) + 8 * (s16 & 1);
-      const uint32_t tb0 = (trow | (zlo + 16 * (lg ^ (q16 >> 1)))) ^ (512 * ch);
-      const uint32_t tb1 = ((trow + 8 * 1024) | (zlo + 16 * (lg ^ (2 + (q16 >> 1))))) ^ (512 * ch);
+      // 16ks + 8(j>>2) + 4g2 + (j&3), the S^T accumulator layout).
+      // ct_row_off(rho) = 16ks kRowPitch + ct_row_off(rho - 16ks), so read x
+      // is lane base tb_x plus the immediate 16ks kRowPitch + 64nb; this
+      // wave's column blocks are nb = 8ch + cb.
+      const uint32_t tcol = cur + 32 * (q16 & 1) + 8 * (s16 & 3) + 512 * ch;
+      const uint32_t tb0 = tcol + ct_row_off(4 * (q16 >> 1) + (s16 >> 2));
+      const uint32_t tb1 = tcol + ct_row_off(8 + 4 * (q16 >> 1) + (s16 >> 2));
       TrPair tr[kPvDepth];
       auto b_issue = [&](TrPair& r, auto step_c) {
         constexpr int step = decltype(step_c)::value;
         constexpr int ks = step >> 3, cb = step & 7;
-        r.x0 = lds_tr<16384 * ks>(L, tb0 ^ (64 * cb));
-        r.x1 = lds_tr<16384 * ks>(L, tb1 ^ (64 * cb));
+        r.x0 = lds_tr<16 * kRowPitch * ks + 64 * cb>(L, tb0);
+        r.x1 = lds_tr<16 * kRowPitch * ks + 64 * cb>(L, tb1);
       };
 
       f32x16 s_next;
       vec ar[kQkDepth];
       vec qr[4];
       vec pp[2];  // partner's P(t), read at step kQrAt
-      static_for<kQkDepth>([&](auto i) { ar[decltype(i)::value] = lds_rd128<vec>(L, a_off(decltype(i)::value)); });
+      static_for<kQkDepth>([&](auto i) { ar[decltype(i)::value] = a_rd(i); });
       static_for<36>([&](auto kk_c) {
         constexpr int kk = decltype(kk_c)::value;
         constexpr int D = kQkDepth;
@@ -698,10 +729,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         } else {
           O_::mma_v(s_next, a, qr[kk - 32]);
         }
-        if constexpr (kk + D < 36) a = lds_rd128<vec>(L, a_off(kk + D));
-        if constexpr (kk % 3 == 2 && kk / 3 < kDmaPerWave) {
-          if (do_dma) issue_copy<kk / 3>(p, sg, t + 2, L, dbuf, wave, lane);
-        }
+        if constexpr (kk + D < 36) a = a_rd(std::integral_constant<int, kk + D>());
+        if constexpr (kk % 3 == 2 && kk / 3 < kDmaPerWave) issue_copy<kk / 3>(p, sg, t + 2, L, dbuf, wave, lane, dm);
         if constexpr (kk >= kTrAt && kk - kTrAt < kPvDepth) b_issue(tr[kk - kTrAt], std::integral_constant<int, kk - kTrAt>());
         __builtin_amdgcn_sched_barrier(0);
       });
@@ -829,8 +858,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         sm_piece(std::integral_constant<int, 2 * step + 1>());
         __builtin_amdgcn_sched_barrier(0);
       });
-      if (do_dma) rot_finish<KT>(L, rot);
-      else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(rot.ka), "+v"(rot.kb), "+v"(rot.c), "+v"(rot.s));
+      rot_finish<KT>(L, rot);  // tile t+2, or zero rows past the segment
       // ---- publish P(t+1) and softmax(t+1)'s rescale for the partner ----
       {
         const int npar = (t + 1) & 1;
