@@ -91,7 +91,11 @@ constexpr int kRescaleSlack = 8;       // log2 units before the running max move
 constexpr int kQkDepth = 8;            // score A operands read this many k-steps ahead
 constexpr int kPvSteps = 16;           // PV operand steps: (ks, column block), 2 MFMAs each
 constexpr int kPvDepth = 6;            // value-read pairs in flight (2 reads per step, lgkmcnt <= 15)
-constexpr int kRotStep = 13;           // PV step after which the RoPE reads of tile t+2 are issued
+constexpr int kRotStep = 9;            // PV step after which the RoPE reads of tile t+2 are issued
+constexpr int kRotSlot0 = 24;          // PV slots kRotSlot0 .. +4 rotate and store them
+// Copy J of a tile goes out at QK step 3i + 2 for i with J = dma_order(i):
+// k_rope, cos and sin first, so the RoPE of the tile only waits for those.
+constexpr int dma_order(int i) { return (i + 8) % 11; }
 constexpr int kQrAt = 32 - kQkDepth;   // QK step before which the q_rope and partner-P reads are issued
 constexpr int kTrAt = 36 - kPvDepth;   // QK steps kTrAt.. issue the first kPvDepth PV value-read pairs
 constexpr int kSmSettle = 1;           // softmax slot (two per PV step) that starts softmax(t+1)
@@ -484,6 +488,19 @@ __device__ inline void rot_finish(lchar* L, RotIn& in) {
 }
 
 template <typename KT>
+__device__ inline void rot_store(lchar* L, const RotIn& in, const float (&ra)[4], const float (&rb)[4]) {
+  typedef typename Ops<KT>::elem E;
+  i16x4 a, b;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    a[e] = __builtin_bit_cast(short, (E)ra[e]);
+    b[e] = __builtin_bit_cast(short, (E)rb[e]);
+  }
+  lds_st(L, in.pa, a);
+  lds_st(L, in.pb, b);
+}
+
+template <typename KT>
 __device__ inline void rotate_rows(lchar* L, uint32_t buf, int wave, int lane) {
   RotIn r = rot_issue(L, buf, wave, lane);
   rot_finish<KT>(L, r);
@@ -631,6 +648,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       }
     }
     for (int t = -1; t < ntiles; ++t) {
+      wait_vm<0>();   // this wave's copies of tile t+1 (issued in iteration t-1) have landed
       lds_barrier();  // tile t+1 staged and rotated by every wave; iteration t-1 done
       const int lane = lane_id();
       const int g2 = lane >> 5;
@@ -730,7 +748,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           O_::mma_v(s_next, a, qr[kk - 32]);
         }
         if constexpr (kk + D < 36) a = a_rd(std::integral_constant<int, kk + D>());
-        if constexpr (kk % 3 == 2 && kk / 3 < kDmaPerWave) issue_copy<kk / 3>(p, sg, t + 2, L, dbuf, wave, lane, dm);
+        if constexpr (kk % 3 == 2 && kk / 3 < kDmaPerWave)
+          issue_copy<dma_order(kk / 3)>(p, sg, t + 2, L, dbuf, wave, lane, dm);
         if constexpr (kk >= kTrAt && kk - kTrAt < kPvDepth) b_issue(tr[kk - kTrAt], std::integral_constant<int, kk - kTrAt>());
         __builtin_amdgcn_sched_barrier(0);
       });
@@ -824,10 +843,27 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // pv_later: LDS operations complete in order), runs the own-head and the
       // partner-head MFMA on them, then issues the reads of step s + kPvDepth
       // into the freed ring slot. After step kRotStep the four RoPE reads of
-      // tile t+2 go out (always; dropped without a tile). Softmax(t+1) takes
-      // two slots per step.
+      // tile t+2 go out (once this wave's k_rope, cos and sin copies have
+      // landed; past the segment they rotate the clamped rows of a tile that
+      // is never used). Softmax(t+1) and the rotation take two slots per step.
       operands_ready(p_cur[0], p_cur[1]);
       RotIn rot;
+      float rot_a[4], rot_b[4];
+      auto rot_piece = [&](auto slot_c) {
+        constexpr int slot = decltype(slot_c)::value;
+        constexpr int e = slot - kRotSlot0;
+        if constexpr (e == 0)
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(rot.ka), "+v"(rot.kb), "+v"(rot.c), "+v"(rot.s));
+        if constexpr (e >= 0 && e < 4) {
+          const float k0 = (float)__builtin_bit_cast(E, (short)rot.ka[e]);
+          const float k1 = (float)__builtin_bit_cast(E, (short)rot.kb[e]);
+          rot_a[e] = k0 * rot.c[e] - k1 * rot.s[e];
+          rot_b[e] = k0 * rot.s[e] + k1 * rot.c[e];
+          asm volatile("" : "+v"(rot_a[e]), "+v"(rot_b[e]));
+        } else if constexpr (e == 4) {
+          rot_store<KT>(L, rot, rot_a, rot_b);
+        }
+      };
       static_for<kPvSteps>([&](auto step_c) {
         constexpr int step = decltype(step_c)::value;
         constexpr int ks = step >> 3, cb = step & 7;
@@ -848,17 +884,18 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         O_::mma_a(acc[cb], p_cur[ks], bvec);
         __builtin_amdgcn_sched_barrier(0);
         sm_piece(std::integral_constant<int, 2 * step>());
+        rot_piece(std::integral_constant<int, 2 * step>());
         __builtin_amdgcn_sched_barrier(0);
         O_::mma_a(acc[8 + cb], pp[ks], bvec);
         if constexpr (step + kPvDepth < kPvSteps) b_issue(bc, std::integral_constant<int, step + kPvDepth>());
         if constexpr (step == kRotStep) {
-          wait_vm<0>();  // this wave's copies of tile t+2 have landed
+          wait_vm<kDmaPerWave - 3>();  // this wave's k_rope / cos / sin copies of tile t+2 have landed
           rot = rot_issue(L, dbuf, wave, lane);
         }
         sm_piece(std::integral_constant<int, 2 * step + 1>());
+        rot_piece(std::integral_constant<int, 2 * step + 1>());
         __builtin_amdgcn_sched_barrier(0);
       });
-      rot_finish<KT>(L, rot);  // tile t+2, or zero rows past the segment
       // ---- publish P(t+1) and softmax(t+1)'s rescale for the partner ----
       {
         const int npar = (t + 1) & 1;
@@ -874,6 +911,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       }
     }
 
+    wait_vm<0>();  // the last iteration's copies (of a tile past the segment) have landed
     // ---- segment end: l over both lane halves; write the slot ----
     // This wave holds the pair's 64 heads (own: acc[0..7], partner:
     // acc[8..15]) over column half ch. Rows go out unnormalised as fp16
