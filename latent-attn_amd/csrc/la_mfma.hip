@@ -92,14 +92,14 @@ constexpr int kQkDepth = 8;            // score A operands read this many k-step
 constexpr int kPvSteps = 16;           // PV operand steps: (ks, column block), 2 MFMAs each
 constexpr int kPvDepth = 6;            // value-read pairs in flight (2 reads per step, lgkmcnt <= 15)
 constexpr int kRotStep = 9;            // PV step after which the RoPE reads of tile t+2 are issued
-constexpr int kRotSlot0 = 24;          // PV slots kRotSlot0 .. +4 rotate and store them
+constexpr int kRotSlot0 = 26;          // PV slots kRotSlot0 .. +5 rotate and store them
 // Copy J of a tile goes out at QK step 3i + 2 for i with J = dma_order(i):
 // k_rope, cos and sin first, so the RoPE of the tile only waits for those.
 constexpr int dma_order(int i) { return (i + 8) % 11; }
 constexpr int kQrAt = 32 - kQkDepth;   // QK step before which the q_rope and partner-P reads are issued
 constexpr int kTrAt = 36 - kPvDepth;   // QK steps kTrAt.. issue the first kPvDepth PV value-read pairs
 constexpr int kSmSettle = 1;           // softmax slot (two per PV step) that starts softmax(t+1)
-constexpr int kSmExp0 = 8;             // softmax slots kSmExp0 .. +15 take one exp2 each
+constexpr int kSmExp0 = 8;             // softmax slots kSmExp0 .. +17: the 3-stage exp2 pipeline
 
 // LDS issue order of one iteration (all reads counted by lgkmcnt):
 //   QK:  [partner flag] A(0..D-1); per step kk: [kk == kQrAt: 4 q_rope
@@ -356,6 +356,21 @@ __device__ inline void wait_lgkm(i16x4& a, i16x4& b, V& c, V& d) {
   static_assert(N >= 0 && N < 16, "lgkmcnt range");
   asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N));
 }
+__device__ inline float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// c + p.x + p.y for a pair of 16-bit P values (v_dot2 with (1, 1))
+__device__ inline float dot2_e(__bf16 __attribute__((ext_vector_type(2))) p, float c) {
+  const __bf16 __attribute__((ext_vector_type(2))) one = {(__bf16)1.f, (__bf16)1.f};
+  return __builtin_amdgcn_fdot2_f32_bf16(p, one, c, false);
+}
+__device__ inline float dot2_e(_Float16 __attribute__((ext_vector_type(2))) p, float c) {
+  const _Float16 __attribute__((ext_vector_type(2))) one = {(_Float16)1.f, (_Float16)1.f};
+  return __builtin_amdgcn_fdot2(p, one, c, false);
+}
+
 // Marks v as produced here (no code): for a value read by inline asm whose
 // completion an earlier, later-issued wait already guarantees.
 template <typename V>
@@ -761,11 +776,11 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // top of the next iteration, after PV(t) has added P(t) . V(t) at the
       // old scale.
       const int valid = min(kT, seg_len - (t + 1) * kT);
-      float m4[4];
+      float mx[5];
       float lmax = -INFINITY;
       uint32_t pw_next[8];  // P(t+1) as bf16/fp16 pairs: word j = positions 2j, 2j+1 of the lane's 16
       float lpart[4];
-      float x_even = 0.f;
+      float sd[16], sx[16];  // s - m and 2^(s - m), one slot apart
       auto sm_piece = [&](auto step_c) {
         constexpr int step = decltype(step_c)::value;
         if constexpr (step == kSmSettle) {
@@ -778,10 +793,25 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
             }
           }
         } else if constexpr (step >= kSmSettle + 1 && step <= kSmSettle + 4) {
+          // max over the lane's 16 scores: a tree of v_max3 (inline asm: the
+          // compiler would canonicalise every operand of fmaxf first), two
+          // independent ops per slot
           constexpr int q = step - kSmSettle - 1;
-          m4[q] = fmaxf(fmaxf(s_next[4 * q], s_next[4 * q + 1]), fmaxf(s_next[4 * q + 2], s_next[4 * q + 3]));
+          if constexpr (q == 0) {
+            mx[0] = max3f(s_next[0], s_next[1], s_next[2]);
+            mx[1] = max3f(s_next[3], s_next[4], s_next[5]);
+          } else if constexpr (q == 1) {
+            mx[2] = max3f(s_next[6], s_next[7], s_next[8]);
+            mx[3] = max3f(s_next[9], s_next[10], s_next[11]);
+          } else if constexpr (q == 2) {
+            mx[4] = max3f(s_next[12], s_next[13], s_next[14]);
+            mx[0] = max3f(mx[0], mx[1], s_next[15]);
+          } else {
+            mx[1] = max3f(mx[2], mx[3], mx[4]);
+          }
+          asm volatile("" : "+v"(mx[0]), "+v"(mx[1]), "+v"(mx[2]), "+v"(mx[3]), "+v"(mx[4]));
         } else if constexpr (step == kSmSettle + 5) {
-          lmax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+          lmax = max3f(mx[0], mx[1], mx[1]);
           const bool need = sm && lmax > m_run + (float)kRescaleSlack;
           if (__builtin_amdgcn_ballot_w64(need) != 0) {
             const float tmax = max_halves(lmax);
@@ -793,27 +823,33 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
             alpha_pend = alpha;
             resc_pend = __builtin_amdgcn_ballot_w64(!first && alpha != 1.f) != 0;
           }
-        } else if constexpr (step >= kSmExp0 && step < kSmExp0 + 16) {
-          // P = 2^(s - m) <= 2^kRescaleSlack; masked and far-below-max scores give 0
-          // The empty asm statements hold each exp and each finished pair of
-          // P in this slot: without them the compiler sinks the whole exp
-          // chain past the PV loop (its only uses are after it), where no
-          // MFMA hides it. l sums the fp32 exps; PV uses them rounded to E
-          // (unbiased rounding, relative error <= 2^-9 per term).
-          constexpr int i = step - kSmExp0;
-          float x = __builtin_amdgcn_exp2f(s_next[i] - m_run);
-          if constexpr (i < 4) lpart[i] = x;
-          else lpart[i & 3] += x;
-          asm volatile("" : "+v"(x), "+v"(lpart[i & 3]));
-          if constexpr ((i & 1) == 0) {
-            x_even = x;
-          } else {
+        } else if constexpr (step >= kSmExp0 && step < kSmExp0 + 18) {
+          // P = 2^(s - m) <= 2^kRescaleSlack; masked and far-below-max scores
+          // give 0. A 3-stage pipeline over the 16 scores, one per slot:
+          // slot j subtracts for score j, exponentiates score j-1 and packs /
+          // sums the pair ending at j-2, so no op waits on another in its
+          // slot. The empty asm statements hold each result in its slot:
+          // without them the compiler sinks the chain past the PV loop (its
+          // only uses are after it), where no MFMA hides it. l sums P as
+          // rounded to E (the values PV uses), two at a time with v_dot2.
+          constexpr int j = step - kSmExp0;
+          if constexpr (j >= 2 && ((j - 2) & 1)) {
+            constexpr int i = j - 2;
             typedef E E2 __attribute__((ext_vector_type(2)));
-            const E2 pr = {(E)x_even, (E)x};
+            const E2 pr = {(E)sx[i - 1], (E)sx[i]};
             pw_next[i >> 1] = __builtin_bit_cast(uint32_t, pr);
-            asm volatile("" : "+v"(pw_next[i >> 1]));
+            lpart[(i >> 1) & 3] = dot2_e(pr, i < 8 ? 0.f : lpart[(i >> 1) & 3]);
+            asm volatile("" : "+v"(pw_next[i >> 1]), "+v"(lpart[(i >> 1) & 3]));
           }
-        } else if constexpr (step == kSmExp0 + 16) {
+          if constexpr (j >= 1 && j <= 16) {
+            sx[j - 1] = __builtin_amdgcn_exp2f(sd[j - 1]);
+            asm volatile("" : "+v"(sx[j - 1]));
+          }
+          if constexpr (j < 16) {
+            sd[j] = s_next[j] - m_run;
+            asm volatile("" : "+v"(sd[j]));
+          }
+        } else if constexpr (step == kSmExp0 + 18) {
           if (sm) l_run += (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
         }
       };
@@ -848,21 +884,28 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // is never used). Softmax(t+1) and the rotation take two slots per step.
       operands_ready(p_cur[0], p_cur[1]);
       RotIn rot;
-      float rot_a[4], rot_b[4];
+      float rot_k0[4], rot_k1[4], rot_a[4], rot_b[4];
       auto rot_piece = [&](auto slot_c) {
-        constexpr int slot = decltype(slot_c)::value;
-        constexpr int e = slot - kRotSlot0;
-        if constexpr (e == 0)
+        // slot r: widen pair e = 2r, 2r+1 (r < 2); products of pair r-1,
+        // sums of pair r-2; the last slot stores
+        constexpr int r = decltype(slot_c)::value - kRotSlot0;
+        if constexpr (r == 0)
           asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(rot.ka), "+v"(rot.kb), "+v"(rot.c), "+v"(rot.s));
-        if constexpr (e >= 0 && e < 4) {
-          const float k0 = (float)__builtin_bit_cast(E, (short)rot.ka[e]);
-          const float k1 = (float)__builtin_bit_cast(E, (short)rot.kb[e]);
-          rot_a[e] = k0 * rot.c[e] - k1 * rot.s[e];
-          rot_b[e] = k0 * rot.s[e] + k1 * rot.c[e];
-          asm volatile("" : "+v"(rot_a[e]), "+v"(rot_b[e]));
-        } else if constexpr (e == 4) {
-          rot_store<KT>(L, rot, rot_a, rot_b);
+        if constexpr (r >= 0 && r < 2) {
+#pragma unroll
+          for (int e = 2 * r; e < 2 * r + 2; ++e) {
+            rot_k0[e] = (float)__builtin_bit_cast(E, (short)rot.ka[e]);
+            rot_k1[e] = (float)__builtin_bit_cast(E, (short)rot.kb[e]);
+            asm volatile("" : "+v"(rot_k0[e]), "+v"(rot_k1[e]));
+          }
         }
+        if constexpr (r >= 2 && r < 6) {
+          constexpr int e = r - 2;
+          rot_a[e] = rot_k0[e] * rot.c[e] - rot_k1[e] * rot.s[e];
+          rot_b[e] = rot_k0[e] * rot.s[e] + rot_k1[e] * rot.c[e];
+          asm volatile("" : "+v"(rot_a[e]), "+v"(rot_b[e]));
+        }
+        if constexpr (r == 5) rot_store<KT>(L, rot, rot_a, rot_b);
       };
       static_for<kPvSteps>([&](auto step_c) {
         constexpr int step = decltype(step_c)::value;
