@@ -79,8 +79,7 @@ constexpr int kNBuf = 3;
 // serves every tile.
 constexpr int kCosOff = kNBuf * kBufBytes;
 constexpr int kSinOff = kCosOff + kT * 128;
-constexpr int kQropeOff = kSinOff + kT * 128;         // q rope k-steps: [wave][r][lane] 16 B
-constexpr int kPtabOff = kQropeOff + kHG * kDr * 2;   // P operands: [parity][wave][ks][lane] 16 B
+constexpr int kPtabOff = kSinOff + kT * 128;          // P operands: [parity][wave][ks][lane] 16 B
 constexpr int kPtabPar = kWaves * 2 * 1024;
 constexpr int kAtabWave = 160;                        // per wave: 32 alphas, rescale flag at +128
 constexpr int kAtabOff = kPtabOff + 2 * kPtabPar;     // [parity][wave]
@@ -88,22 +87,22 @@ constexpr int kAtabPar = kWaves * kAtabWave;
 constexpr int kLdsBytes = kAtabOff + 2 * kAtabPar;
 constexpr int kDmaPerWave = 11;        // 8 c_t rows + k_rope + cos + sin
 constexpr int kRescaleSlack = 8;       // log2 units before the running max moves
-constexpr int kQkDepth = 8;            // score A operands read this many k-steps ahead
+constexpr int kQkDepth = 6;            // score A operands read this many k-steps ahead
 constexpr int kPvSteps = 16;           // PV operand steps: (ks, column block), 2 MFMAs each
-constexpr int kPvDepth = 6;            // value-read pairs in flight (2 reads per step, lgkmcnt <= 15)
+constexpr int kPvDepth = 4;            // value-read pairs in flight (2 reads per step, lgkmcnt <= 15)
 constexpr int kRotStep = 9;            // PV step after which the RoPE reads of tile t+2 are issued
 constexpr int kRotSlot0 = 26;          // PV slots kRotSlot0 .. +5 rotate and store them
 // Copy J of a tile goes out at QK step 3i + 2 for i with J = dma_order(i):
 // k_rope, cos and sin first, so the RoPE of the tile only waits for those.
 constexpr int dma_order(int i) { return (i + 8) % 11; }
-constexpr int kQrAt = 32 - kQkDepth;   // QK step before which the q_rope and partner-P reads are issued
+constexpr int kQrAt = 32 - kQkDepth;   // QK step before which the partner-P reads are issued
 constexpr int kTrAt = 36 - kPvDepth;   // QK steps kTrAt.. issue the first kPvDepth PV value-read pairs
 constexpr int kSmSettle = 1;           // softmax slot (two per PV step) that starts softmax(t+1)
 constexpr int kSmExp0 = 8;             // softmax slots kSmExp0 .. +17: the 3-stage exp2 pipeline
 
 // LDS issue order of one iteration (all reads counted by lgkmcnt):
-//   QK:  [partner flag] A(0..D-1); per step kk: [kk == kQrAt: 4 q_rope
-//        reads, 2 partner-P reads] wait A(kk), MFMA, A(kk+D), [kk >= kTrAt:
+//   QK:  [partner flag] A(0..D-1); per step kk: [kk == kQrAt: 2 partner-P
+//        reads] wait A(kk), MFMA, A(kk+D), [kk >= kTrAt:
 //        value-read pair kk-kTrAt];
 //   PV:  per step s: wait pair s, 2 MFMAs, pair s+kPvDepth, [s == kRotStep:
 //        4 RoPE reads].
@@ -117,7 +116,7 @@ constexpr int qk_later(int kk) {
     ++seq;
   }
   for (int k = 0; k <= kk; ++k) {
-    if (k == kQrAt) seq += 6;
+    if (k == kQrAt) seq += 2;
     if (k == kk) return seq - seq_a - 1;
     if (k + D < 36) {
       if (k + D == kk) seq_a = seq;
@@ -581,30 +580,23 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
 
     // Q^T as the B operand: lane holds Q[head][16kk + 8*g2 .. +8], pre-scaled.
     // q_prep is stored in operand order (qprep_index): the wave's 32 rows form
-    // one block and k-step kk is the coalesced 1 KB at element 512kk. The 32
-    // latent k-steps are loaded into VGPRs; the 4 rope k-steps are copied
-    // straight into this wave's 4 KB of the LDS q-rope table (k-step 32 + r at
-    // 1024r, 16 B per lane) to save 16 VGPRs. A wave without valid heads reads
-    // the group's last block (in bounds); lanes of invalid heads are zeroed,
-    // in VGPRs here and in LDS once the copies have landed.
-    vec qb[32];
+    // one block and k-step kk is the coalesced 1 KB at element 512kk. All 36
+    // k-steps (32 latent, 4 rope) stay in VGPRs for the segment. A wave
+    // without valid heads reads the group's last block (in bounds); lanes of
+    // invalid heads are zeroed.
+    vec qb[36];
     const bool q_head_ok = 32 * wave + (lane0 & 31) < hg_heads;
     {
       const int q_lane = lane_id();
       const int wblk = min(32 * wave, (hg_heads - 1) & ~31);
       const int64_t qrow0 = (int64_t)s * qprep_rows_per_seq(p.Hq) + group * kHG + wblk;
       const E* qbase = reinterpret_cast<const E*>(p.q_prep) + qprep_index(qrow0, 0);
-      static_for<4>([&](auto r_c) {
-        constexpr int r = decltype(r_c)::value;
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(qbase) + 1024 * (32 + r) + 16 * q_lane,
-                                         (lds_void*)(L + kQropeOff + 4096 * wave + 1024 * r), 16, 0, 0);
-      });
       const vec* qsrc = reinterpret_cast<const vec*>(qbase) + q_lane;
 #pragma unroll
-      for (int kk = 0; kk < 32; ++kk) qb[kk] = qsrc[64 * kk];
+      for (int kk = 0; kk < 36; ++kk) qb[kk] = qsrc[64 * kk];
       const vec zero = {};
 #pragma unroll
-      for (int kk = 0; kk < 32; ++kk)
+      for (int kk = 0; kk < 36; ++kk)
         if (!q_head_ok) qb[kk] = zero;
     }
 
@@ -620,11 +612,6 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     }
 
     wait_vm<0>();
-    if (!q_head_ok) {
-      const vec zero = {};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) lds_st(L, kQropeOff + 4096 * wave + 1024 * r + 16 * lane0, zero);
-    }
     rotate_rows<KT>(L, 0, wave, lane_id());  // fresh lane index: no spilled addresses
 
     // Software pipeline over tiles; iteration t (from -1):
@@ -712,7 +699,6 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       const int arow = lane & 31;
       const uint32_t ct_x = nxt + ct_row_off(arow) + 16 * g2;
       const uint32_t rp_x = (nxt + kRopeOff + arow * 128) | (16 * (g2 ^ fr(arow)));
-      const uint32_t qr_x = kQropeOff + 4096 * wave + 16 * lane;
       const uint32_t pp_x = kPtabOff + par * kPtabPar + pw * 2048 + 16 * lane;
       const TileDma dm = tile_dma(sg, t + 2, wave, lane);
       auto a_rd = [&](auto kk_c) -> vec {
@@ -741,15 +727,12 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
 
       f32x16 s_next;
       vec ar[kQkDepth];
-      vec qr[4];
       vec pp[2];  // partner's P(t), read at step kQrAt
       static_for<kQkDepth>([&](auto i) { ar[decltype(i)::value] = a_rd(i); });
       static_for<36>([&](auto kk_c) {
         constexpr int kk = decltype(kk_c)::value;
         constexpr int D = kQkDepth;
         if constexpr (kk == kQrAt) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) qr[r] = lds_rd128<vec>(L, qr_x + 1024 * r);
           pp[0] = lds_rd128<vec>(L, pp_x);
           pp[1] = lds_rd128<vec>(L, pp_x + 1024);
         }
@@ -760,7 +743,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           if constexpr (kk == 0) O_::mma_v0(s_next, a, qb[kk]);
           else O_::mma_v(s_next, a, qb[kk]);
         } else {
-          O_::mma_v(s_next, a, qr[kk - 32]);
+          O_::mma_v(s_next, a, qb[kk]);
         }
         if constexpr (kk + D < 36) a = a_rd(std::integral_constant<int, kk + D>());
         if constexpr (kk % 3 == 2 && kk / 3 < kDmaPerWave)
