@@ -85,6 +85,10 @@ constexpr int kAtabWave = 160;                        // per wave: 32 alphas, re
 constexpr int kAtabOff = kPtabOff + 2 * kPtabPar;     // [parity][wave]
 constexpr int kAtabPar = kWaves * kAtabWave;
 constexpr int kLdsBytes = kAtabOff + 2 * kAtabPar;
+// epilogue staging: per wave 64 fp16 half rows (512 B) at a 528-B pitch
+constexpr int kStagePitch = 528;
+constexpr int kStageBytes = 64 * kStagePitch;
+static_assert(kWaves * kStageBytes <= kLdsBytes, "epilogue staging fits the LDS block");
 constexpr int kDmaPerWave = 11;        // 8 c_t rows + k_rope + cos + sin
 constexpr int kRescaleSlack = 8;       // log2 units before the running max moves
 constexpr int kQkDepth = 6;            // score A operands read this many k-steps ahead
@@ -354,6 +358,12 @@ template <int N, typename V>
 __device__ inline void wait_lgkm(i16x4& a, i16x4& b, V& c, V& d) {
   static_assert(N >= 0 && N < 16, "lgkmcnt range");
   asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N));
+}
+// max(|a|, |b|, c)
+__device__ inline float max3abs(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, |%1|, |%2|, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
 }
 __device__ inline float max3f(float a, float b, float c) {
   float r;
@@ -625,7 +635,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     // waves pair up (w, w^1): each holds O for the pair's 64 heads over one
     // half of the latent columns (256 * (w & 1) ..), so it reads half of the
     // value tile and takes the partner's P(t) from LDS. acc[cb] holds own
-    // heads, acc[8 + cb] the partner's, column block cb of the half.
+    // heads, acc[8 + cb] the partner's, column block cb of the half, transposed
+    // (lane = head).
     // Buffers: tile k lives in buffer k % 3. In iteration t, V(t) and K(t+1)
     // are read and tile t+2 is written; t+2 = t-1 (mod 3) was last read in
     // iteration t-1, before the barrier that opens iteration t. P and rescale
@@ -664,21 +675,14 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       const uint32_t atab = kAtabOff + par * kAtabPar;
 
       // ---- own-head O rows *= alpha where softmax(t) moved the running max ----
-      // O rows are heads 8(i/4) + 4*g2 + (i%4); alpha of head h was published
-      // by this wave (lane h) at the end of iteration t-1.
+      // O is held transposed (lane = head), so the factor is this lane's own
+      // alpha from softmax(t).
       if (resc_pend) {
         settle_acc(acc);
-        f32x16 a16;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f32x4 a4 = lds_ld<f32x4>(L, atab + wave * kAtabWave + 4 * (8 * q + 4 * g2));
-#pragma unroll
-          for (int r = 0; r < 4; ++r) a16[4 * q + r] = a4[r];
-        }
         // one 16-register block at a time, pinned back to AGPRs after each
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) {
-          acc[nb] *= a16;
+          acc[nb] *= alpha_pend;
           pin_agpr(acc[nb]);
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -840,25 +844,22 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
 
       // ---- partner-head O rows *= alpha where the partner's softmax(t) moved its max ----
       if (__builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, pflag)) != 0) {
-        f32x16 a16;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f32x4 a4 = lds_ld<f32x4>(L, atab + pw * kAtabWave + 4 * (8 * q + 4 * g2));
-#pragma unroll
-          for (int r = 0; r < 4; ++r) a16[4 * q + r] = a4[r];
-        }
+        const float a1 = lds_ld<float>(L, atab + pw * kAtabWave + 4 * (lane & 31));  // partner head lane%32
         settle_acc(acc);
 #pragma unroll
         for (int nb = 8; nb < 16; ++nb) {
-          acc[nb] *= a16;
+          acc[nb] *= a1;
           pin_agpr(acc[nb]);
           __builtin_amdgcn_sched_barrier(0);
         }
         acc_ready(acc);
       }
 
-      // ---- PV(t): O[head][c] += P[head][pos] . V[pos][c] over the pair's 64 heads ----
-      // Step s = (ks, column block cb) waits for its value reads (count from
+      // ---- PV(t): O^T[c][head] += V^T[c][pos] . P^T[pos][head] over the pair's 64 heads ----
+      // The value operand goes in as A and P as B, so the accumulators hold O
+      // transposed: lane = head, register i of block cb = column 32cb +
+      // 8(i/4) + 4g2 + (i%4) of this wave's half (a per-head factor is a
+      // per-lane scalar). Step s = (ks, column block cb) waits for its value reads (count from
       // pv_later: LDS operations complete in order), runs the own-head and the
       // partner-head MFMA on them, then issues the reads of step s + kPvDepth
       // into the freed ring slot. After step kRotStep the four RoPE reads of
@@ -907,12 +908,12 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         // leave the pipe, so VALU work placed between the two MFMAs runs while
         // the first executes; placed after both it would wait for the second
         // to issue.
-        O_::mma_a(acc[cb], p_cur[ks], bvec);
+        O_::mma_a(acc[cb], bvec, p_cur[ks]);
         __builtin_amdgcn_sched_barrier(0);
         sm_piece(std::integral_constant<int, 2 * step>());
         rot_piece(std::integral_constant<int, 2 * step>());
         __builtin_amdgcn_sched_barrier(0);
-        O_::mma_a(acc[8 + cb], pp[ks], bvec);
+        O_::mma_a(acc[8 + cb], bvec, pp[ks]);
         if constexpr (step + kPvDepth < kPvSteps) b_issue(bc, std::integral_constant<int, step + kPvDepth>());
         if constexpr (step == kRotStep) {
           wait_vm<kDmaPerWave - 3>();  // this wave's k_rope / cos / sin copies of tile t+2 have landed
@@ -940,10 +941,12 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     wait_vm<0>();  // the last iteration's copies (of a tile past the segment) have landed
     // ---- segment end: l over both lane halves; write the slot ----
     // This wave holds the pair's 64 heads (own: acc[0..7], partner:
-    // acc[8..15]) over column half ch. Rows go out unnormalised as fp16
-    // N * 2^-e per half row, 2^(e-1) <= max_c |N[c]| < 2^e (every value below 1
-    // in magnitude, 11 significant bits relative to the half-row max): no
-    // value crosses waves. The softmax owner writes m and m + log2(l).
+    // acc[8..15]) over column half ch, transposed: lane = head (lane%32),
+    // register i of block cb = column 32cb + 8(i/4) + 4g2 + (i%4). Each head's
+    // half row goes out unnormalised as fp16 N * 2^-e, 2^(e-1) <= max |N| <
+    // 2^e (every value below 1 in magnitude, 11 significant bits relative to
+    // the half-row max); the max is lane-local over 128 values, then over the
+    // two lane halves. The softmax owner writes m and m + log2(l).
     settle_acc(acc);
     const int le = lane_id();  // fresh: the prologue's lane index would come back from a spill slot
     const int g2 = le >> 5;
@@ -954,96 +957,72 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       p.part_lse[hqg + 32 * wave + le] = m_run + log2f(l_tot);
       p.part_m[hqg + 32 * wave + le] = m_run;
     }
-    // register i of a block: row 8(i/4) + 4*g2 + (i%4), column lane%32 of the block.
-    f32x16 am0 = {}, am1 = {};
+    float mo = 0.f, mp = 0.f;
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb) {
       const f32x16 a = acc[cb], b = acc[8 + cb];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        am0[i] = fmaxf(am0[i], fabsf(a[i]));
-        am1[i] = fmaxf(am1[i], fabsf(b[i]));
+      for (int i = 0; i < 16; i += 2) {
+        mo = max3abs(a[i], a[i + 1], mo);
+        mp = max3abs(b[i], b[i + 1], mp);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    f32x16 mul0, mul1;
-    float sc0 = 1.f, sc1 = 1.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {  // max over the 32 lanes (columns) of this half, then the scale
-      const int e0 = __builtin_amdgcn_frexp_expf(max32(am0[i]));  // 0 for a zero row
-      const int e1 = __builtin_amdgcn_frexp_expf(max32(am1[i]));
-      mul0[i] = __builtin_amdgcn_ldexpf(1.f, -e0);
-      mul1[i] = __builtin_amdgcn_ldexpf(1.f, -e1);
-      if ((le & 31) == i) {
-        sc0 = __builtin_amdgcn_ldexpf(1.f, e0);
-        sc1 = __builtin_amdgcn_ldexpf(1.f, e1);
-      }
+    mo = max_halves(mo);
+    mp = max_halves(mp);
+    const int eo = __builtin_amdgcn_frexp_expf(mo);  // 0 for a zero row
+    const int ep = __builtin_amdgcn_frexp_expf(mp);
+    if (le < 32) {
+      if (32 * wave + le < hg_heads) p.part_scale[2 * (hqg + 32 * wave + le) + ch] = __builtin_amdgcn_ldexpf(1.f, eo);
+      if (32 * pw + le < hg_heads) p.part_scale[2 * (hqg + 32 * pw + le) + ch] = __builtin_amdgcn_ldexpf(1.f, ep);
     }
-    if ((le & 31) < 16) {
-      const int i = le & 31;
-      const int hh = 8 * (i >> 2) + 4 * g2 + (i & 3);
-      if (32 * wave + hh < hg_heads) p.part_scale[2 * (hqg + 32 * wave + hh) + ch] = sc0;
-      if (32 * pw + hh < hg_heads) p.part_scale[2 * (hqg + 32 * pw + hh) + ch] = sc1;
-    }
+    const float mulo = __builtin_amdgcn_ldexpf(1.f, -eo), mulp = __builtin_amdgcn_ldexpf(1.f, -ep);
     // Write-out through LDS (the tile buffers are idle now): each wave stages
-    // its two 32-head blocks as fp16 T_b[column][32 heads] (64-B rows, 16 KB
-    // each) with 8-B writes of the 4 consecutive heads a lane holds per
-    // column, then reads rows of O back with ds_read_b64_tr_b16 (two reads =
-    // 8 columns of one head per lane) and stores 16 B per lane.
+    // its 64 half rows as fp16 rows of kStagePitch bytes (own heads 0..31,
+    // then the partner's), 8-B writes of the 4 consecutive columns a lane
+    // holds per (block, i/4); then each round reads two whole rows back (16 B
+    // per lane) and stores them: every store instruction writes eight full
+    // 128-B lines.
     lds_barrier();  // every wave has finished with the tile buffers
-    const uint32_t tbase = 32768 * wave;
+    const uint32_t sbase = kStageBytes * wave;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
       for (int cb = 0; cb < 8; ++cb) {
-        const f32x16 v = acc[8 * b + cb] * (b == 0 ? mul0 : mul1);
+        const f32x16 v = acc[8 * b + cb] * (b == 0 ? mulo : mulp);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           i16x4 h4;
 #pragma unroll
           for (int r = 0; r < 4; ++r) h4[r] = __builtin_bit_cast(short, (_Float16)v[4 * q + r]);
-          lds_st(L, tbase + 16384 * b + (32 * cb + (le & 31)) * 64 + (8 * q + 4 * g2) * 2, h4);
+          lds_st(L, sbase + (32 * b + (le & 31)) * kStagePitch + (32 * cb + 8 * q + 4 * g2) * 2, h4);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes before its reads
     {
-      // tr read x of round j (block b = j / 16, jj = j % 16): lane (q16, s16)
-      // supplies T_b[r0 + s16/4][c0 + 4(s16%4)] with r0 = 16jj + 8(q16>>1) + 4x,
-      // c0 = 16(q16&1); lane i of the group gets T_b[r0 + v][c0 + i], v = 0..3,
-      // i.e. columns r0..r0+3 of head c0 + i of the block.
       const int lr = lane_id();  // fresh index: values derived earlier would come back from spill slots
-      const int q16 = lr >> 4, s16 = lr & 15;
-      const int hl = 16 * (q16 & 1) + s16;
-      const uint32_t rd = tbase + (8 * (q16 >> 1) + (s16 >> 2)) * 64 + (16 * (q16 & 1) + 4 * (s16 & 3)) * 2;
-      _Float16* const obase = reinterpret_cast<_Float16*>(p.part_o) + hqg * kDc + 256 * ch;  // wave-uniform
-      // all 64 reads in flight (each round in its own registers, so no store
+      const uint32_t rd = sbase + (lr >> 5) * kStagePitch + 16 * (lr & 31);
+      _Float16* const obase = reinterpret_cast<_Float16*>(p.part_o) + hqg * kDc + 256 * ch + 8 * (lr & 31);
+      // all 32 reads in flight (each round in its own registers, so no store
       // source is overwritten while the store may still read it), one wait,
       // then the 32 stores back to back
-      i16x4 xa[32], xb[32];
+      i16x8 xr[32];
       static_for<32>([&](auto j_c) {
         constexpr int j = decltype(j_c)::value;
-        constexpr uint32_t off = 16384 * (j >> 4) + (j & 15) * 16 * 64;
-        xa[j] = lds_tr<off>(L, rd);
-        xb[j] = lds_tr<off + 4 * 64>(L, rd);
+        xr[j] = lds_rd128<i16x8, 2 * kStagePitch * j>(L, rd);
       });
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xa[0]), "+v"(xa[1]), "+v"(xa[2]), "+v"(xa[3]), "+v"(xa[4]), "+v"(xa[5]), "+v"(xa[6]), "+v"(xa[7]), "+v"(xb[0]), "+v"(xb[1]), "+v"(xb[2]), "+v"(xb[3]), "+v"(xb[4]), "+v"(xb[5]), "+v"(xb[6]), "+v"(xb[7]));
-      // the waits above cover every read: the rest are ties only
-      asm volatile("" : "+v"(xa[8]), "+v"(xa[9]), "+v"(xa[10]), "+v"(xa[11]), "+v"(xa[12]), "+v"(xa[13]), "+v"(xa[14]), "+v"(xa[15]), "+v"(xb[8]), "+v"(xb[9]), "+v"(xb[10]), "+v"(xb[11]), "+v"(xb[12]), "+v"(xb[13]), "+v"(xb[14]), "+v"(xb[15]));
-      asm volatile("" : "+v"(xa[16]), "+v"(xa[17]), "+v"(xa[18]), "+v"(xa[19]), "+v"(xa[20]), "+v"(xa[21]), "+v"(xa[22]), "+v"(xa[23]), "+v"(xb[16]), "+v"(xb[17]), "+v"(xb[18]), "+v"(xb[19]), "+v"(xb[20]), "+v"(xb[21]), "+v"(xb[22]), "+v"(xb[23]));
-      asm volatile("" : "+v"(xa[24]), "+v"(xa[25]), "+v"(xa[26]), "+v"(xa[27]), "+v"(xa[28]), "+v"(xa[29]), "+v"(xa[30]), "+v"(xa[31]), "+v"(xb[24]), "+v"(xb[25]), "+v"(xb[26]), "+v"(xb[27]), "+v"(xb[28]), "+v"(xb[29]), "+v"(xb[30]), "+v"(xb[31]));
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xr[0]), "+v"(xr[1]), "+v"(xr[2]), "+v"(xr[3]), "+v"(xr[4]), "+v"(xr[5]), "+v"(xr[6]), "+v"(xr[7]));
+      // the wait above covers every read: the rest are ties only
+      asm volatile("" : "+v"(xr[8]), "+v"(xr[9]), "+v"(xr[10]), "+v"(xr[11]), "+v"(xr[12]), "+v"(xr[13]), "+v"(xr[14]), "+v"(xr[15]));
+      asm volatile("" : "+v"(xr[16]), "+v"(xr[17]), "+v"(xr[18]), "+v"(xr[19]), "+v"(xr[20]), "+v"(xr[21]), "+v"(xr[22]), "+v"(xr[23]));
+      asm volatile("" : "+v"(xr[24]), "+v"(xr[25]), "+v"(xr[26]), "+v"(xr[27]), "+v"(xr[28]), "+v"(xr[29]), "+v"(xr[30]), "+v"(xr[31]));
       static_for<32>([&](auto j_c) {
         constexpr int j = decltype(j_c)::value;
-        constexpr int b = j >> 4, jj = j & 15;
-        i16x8 row;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          row[e] = xa[j][e];
-          row[4 + e] = xb[j][e];
-        }
-        const int hb = 32 * (b == 0 ? wave : pw) + hl;  // head within the group
-        if (hb < hg_heads) *reinterpret_cast<i16x8*>(obase + (uint32_t)(hb * kDc + 16 * jj + 8 * (q16 >> 1))) = row;
+        const int r = 2 * j + (lr >> 5);                       // staged row
+        const int hb = r < 32 ? 32 * wave + r : 32 * pw + (r - 32);  // head within the group
+        if (hb < hg_heads) *reinterpret_cast<i16x8*>(obase + (uint32_t)(hb * kDc)) = xr[j];
       });
     }
     lo = seg_hi;
