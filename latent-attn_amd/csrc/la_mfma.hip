@@ -410,6 +410,11 @@ struct TrPair {
 };
 
 constexpr int kRowBytes = (kDc + kDr) * 2;  // 1152: one packed cache row
+// Cache policy of the cache-row copies: non-temporal (the nt bit of the gfx9.4+
+// cache-policy field). Every row is read exactly once per call; streaming the
+// ~300 MB past the caches keeps the weights, queries and partial slots of the
+// surrounding kernels resident in L2 / the infinity cache.
+constexpr int kStreamPolicy = 2;
 
 struct SegCtx {
   const char* base;  // first byte of the segment's first row
@@ -450,9 +455,10 @@ __device__ inline void issue_copy(const DecodeProblem& p, const SegCtx& sg, int 
   if constexpr (J < 8) {
     const int j = min(J, d.dlast);
     __builtin_amdgcn_global_load_lds(sg.base + (d.ct + (uint32_t)(j * kRowBytes)),
-                                     (lds_void*)(L + buf + ct_row_off(r_first + J)), 16, 0, 0);
+                                     (lds_void*)(L + buf + ct_row_off(r_first + J)), 16, 0, kStreamPolicy);
   } else if constexpr (J == 8) {
-    __builtin_amdgcn_global_load_lds(sg.base + d.rope, (lds_void*)(L + buf + kRopeOff + r_first * 128), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(sg.base + d.rope, (lds_void*)(L + buf + kRopeOff + r_first * 128), 16, 0,
+                                     kStreamPolicy);
   } else {
     const int row = r_first + (lane >> 3);
     const int r = min(k * kT + row, sg.last);
