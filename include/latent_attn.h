@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 1
+#define LA_ABI_VERSION 2
 
 typedef enum la_status {
   LA_SUCCESS = 0,
@@ -125,6 +125,11 @@ typedef struct la_decode_args {
    * after the split-KV attention kernel (profiling); NULL = not recorded. */
   void* decode_event_begin;
   void* decode_event_end;
+  /* profiling: > 1 runs the split-KV attention kernel this many times back to
+   * back between the two events (every launch rewrites the same partial
+   * slots, so the result is unchanged), so the events time launches whose
+   * dispatch overlaps the previous one; 0 or 1 = once. */
+  int32_t decode_repeat;
 } la_decode_args;
 
 /* Human-readable name of an la_status value. */

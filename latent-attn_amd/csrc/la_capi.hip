@@ -68,7 +68,8 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   if (!a || !valid_cfg(&a->cfg)) return LA_ERROR_INVALID_VALUE;
   const int chunk_rows = a->chunk_rows;
   const int variant = a->kernel_variant;
-  if (chunk_rows < 0 || variant < kAuto || variant > kMfma || a->rope_rows < 0) return LA_ERROR_INVALID_VALUE;
+  if (chunk_rows < 0 || variant < kAuto || variant > kMfma || a->rope_rows < 0 || a->decode_repeat < 0)
+    return LA_ERROR_INVALID_VALUE;
   if (a->num_seqs < 0 || a->queries_per_seq < 1 || a->total_rows < 0) return LA_ERROR_INVALID_VALUE;
   if (!valid_dtype(a->kv_dtype) || !valid_dtype(a->w_uv_dtype)) return LA_ERROR_INVALID_VALUE;
   if (!a->seq_offsets && (a->seq_len < 0 || (int64_t)a->num_seqs * a->seq_len > a->total_rows))
@@ -240,11 +241,13 @@ int run(const la_decode_args* a, hipStream_t stream) {
     hipEvent_t ev_b = static_cast<hipEvent_t>(a->decode_event_begin);
     hipEvent_t ev_e = static_cast<hipEvent_t>(a->decode_event_end);
     hipError_t e = hipSuccess;
-    if (plan.mfma) {
+    const int reps = a->decode_repeat > 1 ? a->decode_repeat : 1;
+    if (plan.mfma && reps == 1) {
       e = launch_decode_mfma(p, stream, ev_b, ev_e);  // recorded by the launch itself
     } else {
       if (ev_b) e = hipEventRecord(ev_b, stream);
-      if (e == hipSuccess) e = launch_decode_generic(p, stream);
+      for (int r = 0; r < reps && e == hipSuccess; ++r)
+        e = plan.mfma ? launch_decode_mfma(p, stream, nullptr, nullptr) : launch_decode_generic(p, stream);
       if (e == hipSuccess && ev_e) e = hipEventRecord(ev_e, stream);
     }
     if (e != hipSuccess) return finish(e);

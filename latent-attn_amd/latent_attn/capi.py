@@ -54,6 +54,7 @@ class DecodeArgs(ctypes.Structure):
         ("kernel_variant", ctypes.c_int32),
         ("decode_event_begin", ctypes.c_void_p),
         ("decode_event_end", ctypes.c_void_p),
+        ("decode_repeat", ctypes.c_int32),
     ]
 
 

@@ -23,7 +23,7 @@ def test_library_exports_header_symbols():
     assert {"la_mla_decode", "la_fused_mla", "la_batched_fused_mla", "la_absorb_q"} <= set(names)
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.la_abi_version() == 1
+    assert lib.la_abi_version() == 2
 
 
 def test_status_strings():
