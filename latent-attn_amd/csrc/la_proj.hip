@@ -363,7 +363,9 @@ __global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodePro
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           if (j + u < nb) {
-            const float w0 = __shfl(wlo, j + u, 64), w1 = __shfl(whi, j + u, 64);
+            // slot weights broadcast from lane j + u (wave-uniform index: v_readlane, no LDS)
+            const float w0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wlo), j + u));
+            const float w1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, whi), j + u));
             d[u].fma(lane < 32 ? w0 : w1, o0, o1);
           }
         }
