@@ -16,6 +16,9 @@ Prints ONE JSON line. ``value`` is microseconds per decode step (lower is
 better); ``latent_cache_GBps`` is the whole-step cache read rate; ``roofline``
 is the attention kernel's algorithmic latent-cache bytes (1152 B per sequence
 position, one pass) over its measured duration against 8 TB/s.
+``append_kernel_us`` is one device-side cache append (la_append_kv: one new
+bf16 row per sequence of the batch at its length, plus the query's RoPE),
+averaged over back-to-back calls; it is not part of the decode step.
 ``cpu_baseline`` times this repo's CPU restatement of the reference path
 (oracle/, numpy float32 absorbed math) on a bounded sample of the same
 workload, extrapolated to one step.
@@ -141,6 +144,57 @@ def decode_args(inp, out, capi):
     a.output = out.data_ptr()
     a.cfg = capi.config(inp["cfg"])
     return a
+
+
+def time_append(lib, hip, capi, inp, stream, calls: int = 100) -> float:
+    """Microseconds per la_append_kv call: one bf16 row per sequence of the
+    batch appended at its length into a capacity cache (B, calls + 8, 576),
+    with the query's q_rope rotated for that position; calls back to back
+    on the GPU between one event pair (after 4 untimed calls)."""
+    import torch
+
+    cfg, B = inp["cfg"], inp["B"]
+    dev = inp["kv"].device
+    row = cfg.kv_lora_rank + cfg.qk_rope_head_dim
+    cap = calls + 8
+    kv = torch.zeros(B, cap, row, dtype=torch.bfloat16, device=dev)
+    lens = torch.zeros(B, dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev).manual_seed(1)
+    c_t = torch.randn(B, 1, cfg.kv_lora_rank, generator=g, device=dev).to(torch.bfloat16)
+    k_rope = torch.randn(B, 1, cfg.qk_rope_head_dim, generator=g, device=dev).to(torch.bfloat16)
+    q = inp["q_rope"].clone()
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    a = capi.AppendArgs()
+    a.kv_cache, a.kv_dtype, a.total_rows = kv.data_ptr(), capi.LA_DTYPE_BF16, B * cap
+    a.num_seqs, a.seq_capacity, a.seq_lens = B, cap, lens.data_ptr()
+    a.tokens_per_seq, a.c_t, a.k_rope, a.src_dtype = 1, c_t.data_ptr(), k_rope.data_ptr(), capi.LA_DTYPE_BF16
+    a.q_rope, a.queries_per_seq = q.data_ptr(), 1
+    a.rope_cos, a.rope_sin, a.rope_rows = inp["cos"].data_ptr(), inp["sin"].data_ptr(), inp["cos"].shape[0]
+    a.status, a.cfg = status.data_ptr(), capi.config(cfg)
+
+    def call():
+        st = lib.la_append_kv(ctypes.byref(a), ctypes.c_void_p(stream))
+        if st != 0:
+            raise RuntimeError(f"la_append_kv: {lib.la_status_string(st).decode()}")
+
+    for _ in range(4):
+        call()
+    t0, t1 = new_event(hip), new_event(hip)
+    torch.cuda.synchronize()
+    # A short spin kernel holds the stream while the host enqueues the calls
+    # (~10 us of host time each), so the event pair times the appends back to
+    # back on the GPU rather than the host's launch rate.
+    torch.cuda._sleep(4_000_000)
+    hip.hipEventRecord(t0, ctypes.c_void_p(stream))
+    for _ in range(calls):
+        call()
+    hip.hipEventRecord(t1, ctypes.c_void_p(stream))
+    hip.hipEventSynchronize(t1)
+    us = elapsed_ms(hip, t0, t1) * 1e3 / calls
+    hip.hipEventDestroy(t0)
+    hip.hipEventDestroy(t1)
+    assert status.item() == 0 and int(lens[0].item()) == calls + 4, "append bench overflowed its cache"
+    return us
 
 
 def measured_traffic(config: str):
@@ -297,6 +351,7 @@ def main():
     kern_avg = sum(kern_ms) / KERN_CALLS
     ms_step = ms_total / K
     us_step = ms_step * 1e3
+    append_us = time_append(lib, hip, capi, inp, stream)
 
     total_pos = int(inp["total"])
     cache_bytes = total_pos * BYTES_PER_POS
@@ -332,6 +387,7 @@ def main():
         "attn_kernel_us": round(kern_avg * 1e3, 2),
         "attn_kernel_us_min_max": [round(kern_ms[0] * 1e3, 2), round(kern_ms[-1] * 1e3, 2)],
         "mfma_frac_of_bf16_peak": round(flops_attn / (kern_avg * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "append_kernel_us": round(append_us, 2),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved_gbps, 1),

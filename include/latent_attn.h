@@ -19,6 +19,10 @@
  *                            with log-sum-exp combine, fused W_UV projection)
  *   la_mla_config         <- MLAConfig                 src/mla_config.cuh:7-13
  *                            (same six ints in the same order)
+ *   la_append_kv          <- LatentKVCache::append_host src/mla_config.cuh:57-72
+ *                            (host-to-device copies of one row plus a stream
+ *                            synchronize per token), done on the device for
+ *                            every sequence at once, with the query's RoPE
  *
  * Layouts (all row-major, contiguous):
  *   latent cache row   [c_t (kv_lora_rank) | k_rope (qk_rope_head_dim)]
@@ -48,7 +52,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 2
+#define LA_ABI_VERSION 3
 
 typedef enum la_status {
   LA_SUCCESS = 0,
@@ -130,7 +134,54 @@ typedef struct la_decode_args {
    * slots, so the result is unchanged), so the events time launches whose
    * dispatch overlaps the previous one; 0 or 1 = once. */
   int32_t decode_repeat;
+  /* optional DEVICE int32 array of num_seqs lengths (as la_append_kv keeps
+   * them): sequence s is the first seq_lens[s] rows of its region above
+   * (clamped into it; rows past it are unfilled capacity and are not read).
+   * NULL: each sequence is its whole region. The split plan covers the
+   * regions, so capacity far beyond the lengths costs idle blocks. */
+  const int32_t* seq_lens;
 } la_decode_args;
+
+/* Arguments of la_append_kv. */
+typedef struct la_append_args {
+  /* latent cache, laid out as for la_decode_args: sequence s owns the region
+   * [s*seq_capacity, (s+1)*seq_capacity) (seq_offsets == NULL) or
+   * [seq_offsets[s], seq_offsets[s+1]) (DEVICE int32, num_seqs+1), and its
+   * first seq_lens[s] rows are filled. */
+  void* kv_cache;
+  int32_t kv_dtype; /* la_dtype */
+  int64_t total_rows;
+  int32_t num_seqs;
+  int32_t seq_capacity;
+  const int32_t* seq_offsets;
+  int32_t* seq_lens; /* DEVICE int32, num_seqs; advanced by tokens_per_seq */
+  /* new rows: c_t (num_seqs, tokens_per_seq, kv_lora_rank) and k_rope
+   * (num_seqs, tokens_per_seq, qk_rope_head_dim) in src_dtype, k_rope NOT
+   * rotated (the attention rotates keys by their position, as the
+   * reference's cache holds them). Row j of sequence s lands at position
+   * seq_lens[s] + j. */
+  int32_t tokens_per_seq;
+  const void* c_t;
+  const void* k_rope;
+  int32_t src_dtype; /* la_dtype */
+  /* optional: q_rope (num_seqs*queries_per_seq, num_heads, qk_rope_head_dim)
+   * f32, rotated in place (rotate-half, src/fused_mla.cu:43-51) for its
+   * position: query j of sequence s is the token at position
+   * seq_lens[s] + tokens_per_seq - queries_per_seq + j (the last
+   * queries_per_seq appended tokens; queries_per_seq <= tokens_per_seq).
+   * When qk_rope_head_dim/2 is a multiple of 4, q_rope, rope_cos and rope_sin
+   * must be 16-byte aligned. NULL: no query rotation. */
+  float* q_rope;
+  int32_t queries_per_seq;
+  const float* rope_cos; /* (rope_rows, qk_rope_head_dim/2) f32 */
+  const float* rope_sin;
+  int64_t rope_rows; /* 0 = unchecked; positions past it use the last row */
+  /* optional DEVICE int32: set to 1 when a sequence has no room for
+   * tokens_per_seq more rows (that sequence is left unchanged: no rows, no
+   * length change, no query rotation); never cleared by the library. */
+  int32_t* status;
+  la_mla_config cfg;
+} la_append_args;
 
 /* Human-readable name of an la_status value. */
 const char* la_status_string(int status);
@@ -167,6 +218,12 @@ int la_batched_fused_mla(const void* kv_cache, int kv_dtype, int seq_len, int ba
 /* Workspace bytes la_fused_mla / la_batched_fused_mla need (batch_size 1 for
  * la_fused_mla). */
 size_t la_fused_mla_workspace_size(int seq_len, int batch_size, const la_mla_config* cfg);
+
+/* Appends tokens_per_seq rows to every sequence's cache on the device and
+ * advances seq_lens (replaces LatentKVCache::append_host,
+ * src/mla_config.cuh:57-72: no host copies, no synchronize, no host-side
+ * length), then rotates the queries' q_rope for their positions. */
+int la_append_kv(const la_append_args* args, void* stream);
 
 /* Query absorption q_abs[t,h,c] = sum_i q_nope[t,h,i] * W_UK[h*dn+i, c]
  * (tests/test_correctness.cu:29-46). q_nope (tokens, nh, dn) f32,

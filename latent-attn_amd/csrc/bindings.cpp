@@ -171,11 +171,14 @@ torch::Tensor batched_fused_mla_forward(torch::Tensor kv_cache, torch::Tensor q_
 //   q_nope (B, nh, dn) f32; q_rope (B, nh, dR) f32 (already rotated)
 //   W_UK (nh*dn, dc); W_UV (nh*dv, dc); rope tables (>= longest seq, dR/2)
 //   returns (B, nh, dv) f32. chunk_rows / kernel_variant: tuning overrides.
+//   seq_lens: None or int32 (B,) device tensor; sequence b is the first
+//   seq_lens[b] rows of its region (a capacity cache filled by append_kv).
 torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, torch::Tensor q_rope,
                                  torch::Tensor W_UK, torch::Tensor W_UV, torch::Tensor rope_cos,
                                  torch::Tensor rope_sin, c10::optional<torch::Tensor> seq_offsets, int d_model,
                                  int kv_lora_rank, int qk_nope_head_dim, int qk_rope_head_dim, int num_heads,
-                                 int v_head_dim, int chunk_rows, int kernel_variant) {
+                                 int v_head_dim, int chunk_rows, int kernel_variant,
+                                 c10::optional<torch::Tensor> seq_lens) {
   check_storage(kv_cache, "kv_cache");
   check_fp32_contiguous(q_nope, "q_nope");
   check_fp32_contiguous(q_rope, "q_rope");
@@ -225,6 +228,15 @@ torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, t
     longest = kv_cache.size(1);
     a.rope_rows = rope_cos.size(0);
   }
+  if (seq_lens.has_value() && seq_lens->defined()) {
+    const auto& len = *seq_lens;
+    TORCH_CHECK(len.dtype() == torch::kInt32 && len.is_contiguous() && len.is_cuda(),
+                "seq_lens must be a contiguous int32 CUDA tensor");
+    TORCH_CHECK(len.dim() == 1 && len.size(0) == batch, "seq_lens must have batch entries");
+    check_same_device(kv_cache, len, "seq_lens");
+    a.seq_lens = len.data_ptr<int32_t>();
+    longest = 0;  // lengths live on the device; positions past the table clamp
+  }
   check_rope(rope_cos, rope_sin, longest, cfg);
   for (auto* t : {&q_nope, &q_rope, &W_UK, &W_UV, &rope_cos, &rope_sin}) check_same_device(kv_cache, *t, "inputs");
   a.q_nope = q_nope.data_ptr<float>();
@@ -249,6 +261,98 @@ torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, t
   a.workspace_bytes = ws_bytes;
   check_status(la_mla_decode(&a, current_stream()), "la_mla_decode");
   return output;
+}
+
+// append_kv_forward -- device-side LatentKVCache::append_host
+// (src/mla_config.cuh:57-72) for a batch: appends c_t (B, T, dc) and k_rope
+// (B, T, dR) (one dtype, any of the three) at each sequence's length in
+// kv_cache ((B, capacity, dc+dR), or packed (rows, dc+dR) with seq_offsets
+// (B+1,) int32 regions), advances seq_lens (B,) int32 in place and, when
+// q_rope ((B*qps, nh, dR) f32) is given, rotates it in place for the
+// positions of the last qps appended tokens. status: optional int32 (1,)
+// device flag set to 1 when a sequence has no room.
+void append_kv_forward(torch::Tensor kv_cache, torch::Tensor seq_lens, torch::Tensor c_t, torch::Tensor k_rope,
+                       c10::optional<torch::Tensor> q_rope, c10::optional<torch::Tensor> rope_cos,
+                       c10::optional<torch::Tensor> rope_sin, c10::optional<torch::Tensor> seq_offsets,
+                       c10::optional<torch::Tensor> status, int d_model, int kv_lora_rank, int qk_nope_head_dim,
+                       int qk_rope_head_dim, int num_heads, int v_head_dim) {
+  check_storage(kv_cache, "kv_cache");
+  check_storage(c_t, "c_t");
+  check_storage(k_rope, "k_rope");
+  la_mla_config cfg =
+      config_from_args(d_model, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, num_heads, v_head_dim);
+  const int64_t row = kv_lora_rank + qk_rope_head_dim;
+  TORCH_CHECK(seq_lens.dtype() == torch::kInt32 && seq_lens.is_contiguous() && seq_lens.is_cuda() &&
+                  seq_lens.dim() == 1,
+              "seq_lens must be a contiguous 1D int32 CUDA tensor");
+  const int64_t batch = seq_lens.size(0);
+  TORCH_CHECK(batch <= INT32_MAX, "batch too large");
+  TORCH_CHECK(c_t.dim() == 3 && c_t.size(0) == batch && c_t.size(2) == kv_lora_rank,
+              "c_t must be (batch, tokens, kv_lora_rank)");
+  const int64_t tokens = c_t.size(1);
+  TORCH_CHECK(tokens <= INT32_MAX, "too many tokens");
+  TORCH_CHECK(k_rope.dim() == 3 && k_rope.size(0) == batch && k_rope.size(1) == tokens &&
+                  k_rope.size(2) == qk_rope_head_dim,
+              "k_rope must be (batch, tokens, qk_rope_head_dim)");
+  TORCH_CHECK(k_rope.dtype() == c_t.dtype(), "c_t and k_rope must have the same dtype");
+  for (auto* t : {&seq_lens, &c_t, &k_rope}) check_same_device(kv_cache, *t, "inputs");
+
+  la_append_args a{};
+  a.kv_cache = kv_cache.data_ptr();
+  a.kv_dtype = dtype_tag(kv_cache);
+  a.num_seqs = (int32_t)batch;
+  a.seq_lens = seq_lens.data_ptr<int32_t>();
+  a.tokens_per_seq = (int32_t)tokens;
+  a.c_t = c_t.data_ptr();
+  a.k_rope = k_rope.data_ptr();
+  a.src_dtype = dtype_tag(c_t);
+  a.cfg = cfg;
+  if (seq_offsets.has_value() && seq_offsets->defined()) {
+    const auto& off = *seq_offsets;
+    TORCH_CHECK(off.dtype() == torch::kInt32 && off.is_contiguous() && off.is_cuda(),
+                "seq_offsets must be a contiguous int32 CUDA tensor");
+    TORCH_CHECK(off.dim() == 1 && off.size(0) == batch + 1, "seq_offsets must have batch + 1 entries");
+    check_same_device(kv_cache, off, "seq_offsets");
+    TORCH_CHECK(kv_cache.dim() == 2 && kv_cache.size(1) == row, "packed kv_cache must be (total_rows, ", row, ")");
+    a.total_rows = kv_cache.size(0);
+    a.seq_offsets = off.data_ptr<int32_t>();
+  } else {
+    TORCH_CHECK(kv_cache.dim() == 3 && kv_cache.size(0) == batch && kv_cache.size(2) == row,
+                "kv_cache must be (batch, capacity, ", row, ") when seq_offsets is None");
+    TORCH_CHECK(kv_cache.size(1) <= INT32_MAX, "capacity too large");
+    a.seq_capacity = (int32_t)kv_cache.size(1);
+    a.total_rows = batch * kv_cache.size(1);
+  }
+  if (q_rope.has_value() && q_rope->defined()) {
+    const auto& q = *q_rope;
+    check_fp32_contiguous(q, "q_rope");
+    TORCH_CHECK(batch > 0 && q.dim() == 3 && q.size(0) % batch == 0 && q.size(1) == num_heads &&
+                    q.size(2) == qk_rope_head_dim,
+                "q_rope must be (batch * queries_per_seq, num_heads, qk_rope_head_dim)");
+    TORCH_CHECK(rope_cos.has_value() && rope_sin.has_value() && rope_cos->defined() && rope_sin->defined(),
+                "rope_cos / rope_sin are required with q_rope");
+    check_fp32_contiguous(*rope_cos, "rope_cos");
+    check_fp32_contiguous(*rope_sin, "rope_sin");
+    check_rope(*rope_cos, *rope_sin, 1, cfg);
+    check_same_device(kv_cache, q, "q_rope");
+    check_same_device(kv_cache, *rope_cos, "rope_cos");
+    check_same_device(kv_cache, *rope_sin, "rope_sin");
+    const int64_t qps = q.size(0) / batch;
+    TORCH_CHECK(qps <= tokens, "queries_per_seq (", qps, ") must not exceed the appended tokens (", tokens, ")");
+    a.q_rope = q.data_ptr<float>();
+    a.queries_per_seq = (int32_t)qps;
+    a.rope_cos = rope_cos->data_ptr<float>();
+    a.rope_sin = rope_sin->data_ptr<float>();
+    a.rope_rows = rope_cos->size(0);
+  }
+  if (status.has_value() && status->defined()) {
+    TORCH_CHECK(status->dtype() == torch::kInt32 && status->is_cuda() && status->numel() >= 1,
+                "status must be an int32 CUDA tensor");
+    check_same_device(kv_cache, *status, "status");
+    a.status = status->data_ptr<int32_t>();
+  }
+  const at::DeviceGuard guard(kv_cache.device());
+  check_status(la_append_kv(&a, current_stream()), "la_append_kv");
 }
 
 // absorb_q_forward -- q_abs[t,h,c] = sum_i q_nope[t,h,i] W_UK[h*dn+i, c]
@@ -300,7 +404,7 @@ torch::Tensor naive_mla_forward(torch::Tensor kv_cache, torch::Tensor W_UK, torc
               "q_rope shape mismatch");
   auto out = mla_decode_forward(kv_cache.unsqueeze(0), q_nope.unsqueeze(0), q_rope.unsqueeze(0), W_UK, W_UV,
                                 rope_cos, rope_sin, c10::nullopt, d_model, kv_lora_rank, qk_nope_head_dim,
-                                qk_rope_head_dim, num_heads, v_head_dim, 0, 0);
+                                qk_rope_head_dim, num_heads, v_head_dim, 0, 0, c10::nullopt);
   return out.squeeze(0);
 }
 
@@ -315,6 +419,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("kv_cache"), py::arg("q_nope"), py::arg("q_rope"), py::arg("W_UK"), py::arg("W_UV"),
         py::arg("rope_cos"), py::arg("rope_sin"), py::arg("seq_offsets"), py::arg("d_model"),
         py::arg("kv_lora_rank"), py::arg("qk_nope_head_dim"), py::arg("qk_rope_head_dim"), py::arg("num_heads"),
-        py::arg("v_head_dim"), py::arg("chunk_rows") = 0, py::arg("kernel_variant") = 0);
+        py::arg("v_head_dim"), py::arg("chunk_rows") = 0, py::arg("kernel_variant") = 0,
+        py::arg("seq_lens") = py::none());
+  m.def("append_kv_forward", &append_kv_forward,
+        "Device-side append of latent rows at each sequence's length, with the query's RoPE",
+        py::arg("kv_cache"), py::arg("seq_lens"), py::arg("c_t"), py::arg("k_rope"), py::arg("q_rope"),
+        py::arg("rope_cos"), py::arg("rope_sin"), py::arg("seq_offsets"), py::arg("status"), py::arg("d_model"),
+        py::arg("kv_lora_rank"), py::arg("qk_nope_head_dim"), py::arg("qk_rope_head_dim"), py::arg("num_heads"),
+        py::arg("v_head_dim"));
   m.def("absorb_q_forward", &absorb_q_forward, "q_absorbed = q_nope . W_UK per head");
 }

@@ -87,6 +87,7 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   p->num_seqs = a->num_seqs;
   p->seq_len = a->seq_offsets ? 0 : a->seq_len;
   p->offsets = a->seq_offsets;
+  p->lens = a->seq_lens;
   p->qps = a->queries_per_seq;
   p->nh = c.num_heads;
   p->Hq = a->queries_per_seq * c.num_heads;
@@ -350,6 +351,52 @@ size_t la_fused_mla_workspace_size(int seq_len, int batch_size, const la_mla_con
     }
   }
   return best;
+}
+
+int la_append_kv(const la_append_args* a, void* stream) {
+  if (!a || !la::valid_cfg(&a->cfg) || !la::valid_dtype(a->kv_dtype) || !la::valid_dtype(a->src_dtype))
+    return LA_ERROR_INVALID_VALUE;
+  if (a->num_seqs < 0 || a->tokens_per_seq < 0 || a->total_rows < 0 || a->rope_rows < 0) return LA_ERROR_INVALID_VALUE;
+  if (!a->seq_offsets && (a->seq_capacity < 0 || (int64_t)a->num_seqs * a->seq_capacity > a->total_rows))
+    return LA_ERROR_INVALID_VALUE;
+  if (a->num_seqs == 0) return LA_SUCCESS;
+  if (!a->seq_lens || (a->total_rows > 0 && !a->kv_cache)) return LA_ERROR_INVALID_VALUE;
+  if (a->tokens_per_seq > 0 && (!a->c_t || !a->k_rope)) return LA_ERROR_INVALID_VALUE;
+  // per-sequence element counts stay within the kernel's 32-bit indexing
+  if ((int64_t)a->tokens_per_seq * (a->cfg.kv_lora_rank + a->cfg.qk_rope_head_dim) > INT32_MAX ||
+      (a->q_rope && (int64_t)a->queries_per_seq * a->cfg.num_heads * a->cfg.qk_rope_head_dim > INT32_MAX))
+    return LA_ERROR_INVALID_VALUE;
+  // the vectorised query rotation reads 16-B chunks of q_rope and the tables
+  if (a->q_rope && (a->cfg.qk_rope_head_dim / 2) % 4 == 0 &&
+      ((reinterpret_cast<uintptr_t>(a->q_rope) | reinterpret_cast<uintptr_t>(a->rope_cos) |
+        reinterpret_cast<uintptr_t>(a->rope_sin)) & 15))
+    return LA_ERROR_INVALID_VALUE;
+  if (a->q_rope && (a->queries_per_seq < 1 || a->queries_per_seq > a->tokens_per_seq || !a->rope_cos ||
+                    !a->rope_sin || (int64_t)a->num_seqs * a->queries_per_seq * a->cfg.num_heads > INT32_MAX))
+    return LA_ERROR_INVALID_VALUE;
+  la::AppendProblem p{};
+  p.kv = a->kv_cache;
+  p.kv_dtype = a->kv_dtype;
+  p.total_rows = a->total_rows;
+  p.num_seqs = a->num_seqs;
+  p.capacity = a->seq_offsets ? 0 : a->seq_capacity;
+  p.offsets = a->seq_offsets;
+  p.lens = a->seq_lens;
+  p.tokens = a->tokens_per_seq;
+  p.c_t = a->c_t;
+  p.k_rope = a->k_rope;
+  p.src_dtype = a->src_dtype;
+  p.q_rope = a->q_rope;
+  p.qps = a->q_rope ? a->queries_per_seq : 0;
+  p.nh = a->cfg.num_heads;
+  p.rope_cos = a->rope_cos;
+  p.rope_sin = a->rope_sin;
+  p.rope_rows = a->rope_rows;
+  p.status = a->status;
+  p.dc = a->cfg.kv_lora_rank;
+  p.dR = a->cfg.qk_rope_head_dim;
+  const hipError_t e = la::launch_append(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? (int)LA_SUCCESS : la::record_hip(e);
 }
 
 int la_absorb_q(const float* q_nope, const void* W_UK, int w_uk_dtype, float* q_absorbed, int tokens,

@@ -49,9 +49,12 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
   int s = find_seq(p, lo);
 
   while (lo < hi) {
-    const int64_t s_lo = seq_begin(p, s), s_hi = seq_begin(p, s + 1);
-    if (s_hi <= lo) {  // empty sequence or already consumed
-      ++s;
+    const int64_t s_lo = seq_begin(p, s);
+    lo = max(lo, s_lo);  // past the unfilled rows of the previous region
+    if (lo >= hi) break;
+    const int64_t s_hi = seq_end(p, s);
+    if (s_hi <= lo) {  // empty sequence, already consumed, or lo in its unfilled rows
+      if (++s >= p.num_seqs) break;
       continue;
     }
     const int64_t seg_hi = min(hi, s_hi);
@@ -174,7 +177,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_project_kernel(Decode
       s = r / p.qps;
       hq = (r % p.qps) * p.nh + h;
       lo = seq_begin(p, s);
-      hi = seq_begin(p, s + 1);
+      hi = seq_end(p, s);
     }
     if (hi <= lo) {
       for (int c = lane; c < dc; c += 64) orow[c] = 0.f;

@@ -47,6 +47,7 @@ struct DecodeProblem {
   int num_seqs;
   int seq_len;            // used when offsets == nullptr
   const int32_t* offsets; // device, num_seqs + 1, or nullptr
+  const int32_t* lens;    // device, num_seqs, or nullptr: filled rows of each region
   int qps;                // query tokens per sequence
   int nh;                 // weight heads
   int Hq;                 // query heads per sequence = qps * nh
@@ -92,6 +93,17 @@ __device__ inline float load_part(const DecodeProblem& p, int64_t row, int i) {
 __device__ inline int64_t seq_begin(const DecodeProblem& p, int s) {
   const int64_t b = p.offsets ? (int64_t)p.offsets[s] : (int64_t)s * p.seq_len;
   return b < 0 ? 0 : (b > p.total_rows ? p.total_rows : b);
+}
+
+// End of sequence s's rows: the end of its region, or, with per-sequence
+// lengths, its first row plus its length clamped into the region (the rows
+// past it are unfilled capacity and belong to no sequence).
+__device__ inline int64_t seq_end(const DecodeProblem& p, int s) {
+  const int64_t region_end = seq_begin(p, s + 1);
+  if (!p.lens) return region_end;
+  const int64_t b = seq_begin(p, s);
+  const int64_t l = p.lens[s];
+  return l <= 0 ? b : (b + l < region_end ? b + l : region_end);
 }
 
 // RoPE table row of in-sequence position pos.
@@ -142,7 +154,33 @@ __device__ inline float wave_max(float v) {
   return v;
 }
 
+// One la_append_kv call, resolved on the host (la_append.hip).
+struct AppendProblem {
+  void* kv;
+  int kv_dtype;
+  int64_t total_rows;
+  int num_seqs;
+  int capacity;            // region rows per sequence when offsets == nullptr
+  const int32_t* offsets;  // device, num_seqs + 1, or nullptr
+  int32_t* lens;           // device, num_seqs
+  int tokens;
+  const void* c_t;
+  const void* k_rope;
+  int src_dtype;
+  float* q_rope;           // nullptr = no query rotation
+  int qps;
+  int nh;
+  const float* rope_cos;
+  const float* rope_sin;
+  int64_t rope_rows;
+  int32_t* status;
+  int dc, dR;
+};
+
 // ---- host launchers (one per kernel family) -------------------------------
+
+// Device-side cache append + query RoPE.
+hipError_t launch_append(const AppendProblem& p, hipStream_t stream);
 
 // VALU split-KV decode: any dtype, kv_lora_rank <= 1024, qk_rope_head_dim <= 256.
 hipError_t launch_decode_generic(const DecodeProblem& p, hipStream_t stream);

@@ -574,9 +574,12 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
   int s = find_seq(p, lo);
 
   while (lo < hi) {
-    const int64_t s_lo = seq_begin(p, s), s_hi = seq_begin(p, s + 1);
-    if (s_hi <= lo) {
-      ++s;
+    const int64_t s_lo = seq_begin(p, s);
+    lo = max(lo, s_lo);  // past the unfilled rows of the previous region
+    if (lo >= hi) break;
+    const int64_t s_hi = seq_end(p, s);
+    if (s_hi <= lo) {  // empty sequence, or lo in its unfilled rows
+      if (++s >= p.num_seqs) break;
       continue;
     }
     const int64_t seg_hi = min(hi, s_hi);

@@ -301,7 +301,7 @@ __global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodePro
   const int s = r / p.qps;
   const int hq = (r % p.qps) * p.nh + h;
   f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
-  const int64_t lo = seq_begin(p, s), hi = seq_begin(p, s + 1);
+  const int64_t lo = seq_begin(p, s), hi = seq_end(p, s);
   if (hi > lo) {
     const int64_t cf = lo / p.chunk_len;
     const int n = (int)((hi - 1) / p.chunk_len - cf + 1);  // slots cf+s .. cf+s+n-1

@@ -55,6 +55,30 @@ class DecodeArgs(ctypes.Structure):
         ("decode_event_begin", ctypes.c_void_p),
         ("decode_event_end", ctypes.c_void_p),
         ("decode_repeat", ctypes.c_int32),
+        ("seq_lens", ctypes.c_void_p),
+    ]
+
+
+class AppendArgs(ctypes.Structure):
+    _fields_ = [
+        ("kv_cache", ctypes.c_void_p),
+        ("kv_dtype", ctypes.c_int32),
+        ("total_rows", ctypes.c_int64),
+        ("num_seqs", ctypes.c_int32),
+        ("seq_capacity", ctypes.c_int32),
+        ("seq_offsets", ctypes.c_void_p),
+        ("seq_lens", ctypes.c_void_p),
+        ("tokens_per_seq", ctypes.c_int32),
+        ("c_t", ctypes.c_void_p),
+        ("k_rope", ctypes.c_void_p),
+        ("src_dtype", ctypes.c_int32),
+        ("q_rope", ctypes.c_void_p),
+        ("queries_per_seq", ctypes.c_int32),
+        ("rope_cos", ctypes.c_void_p),
+        ("rope_sin", ctypes.c_void_p),
+        ("rope_rows", ctypes.c_int64),
+        ("status", ctypes.c_void_p),
+        ("cfg", MlaConfig),
     ]
 
 
@@ -89,6 +113,8 @@ def load() -> ctypes.CDLL:
     lib.la_fused_mla_workspace_size.argtypes = [i32, i32, cfgp]
     lib.la_absorb_q.restype = i32
     lib.la_absorb_q.argtypes = [vp, vp, i32, vp, i32, cfgp, vp]
+    lib.la_append_kv.restype = i32
+    lib.la_append_kv.argtypes = [ctypes.POINTER(AppendArgs), vp]
     _lib = lib
     return lib
 

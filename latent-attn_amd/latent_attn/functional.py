@@ -118,6 +118,7 @@ def mla_decode(
     seq_offsets: Optional[torch.Tensor] = None,
     chunk_rows: int = 0,
     kernel_variant: int = 0,
+    seq_lens: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """One decode step for a batch of sequences, each with its own cache.
 
@@ -133,13 +134,54 @@ def mla_decode(
                      rows [seq_offsets[b], seq_offsets[b+1])
         chunk_rows, kernel_variant: tuning overrides (0 = automatic; variant
                      1 = VALU kernel, 2 = MFMA kernel)
+        seq_lens:    optional int32 (batch,) device tensor; sequence b is the
+                     first seq_lens[b] rows of its region (a capacity cache
+                     filled by ``append_kv``)
 
     Returns:
         (batch, num_heads, v_head_dim) fp32
     """
     _C = _load_ext()
     return _C.mla_decode_forward(kv_cache, q_nope, q_rope, W_UK, W_UV, rope_cos, rope_sin, seq_offsets,
-                                 *_cfg_args(cfg), chunk_rows, kernel_variant)
+                                 *_cfg_args(cfg), chunk_rows, kernel_variant, seq_lens)
+
+
+def append_kv(
+    kv_cache: torch.Tensor,
+    seq_lens: torch.Tensor,
+    c_t: torch.Tensor,
+    k_rope: torch.Tensor,
+    cfg: "MLAConfig",
+    q_rope: Optional[torch.Tensor] = None,
+    rope_cos: Optional[torch.Tensor] = None,
+    rope_sin: Optional[torch.Tensor] = None,
+    seq_offsets: Optional[torch.Tensor] = None,
+    status: Optional[torch.Tensor] = None,
+) -> None:
+    """Append new latent rows to every sequence's cache on the device.
+
+    The device-side counterpart of the reference's
+    ``LatentKVCache::append_host`` (src/mla_config.cuh:57-72) for a batch:
+    no host copies and no synchronize; lengths are kept on the device.
+
+    Args:
+        kv_cache:    (batch, capacity, dc + dR) when ``seq_offsets`` is None,
+                     else a packed (rows, dc + dR) cache whose sequence b owns
+                     rows [seq_offsets[b], seq_offsets[b+1])
+        seq_lens:    int32 (batch,) device tensor of filled rows, advanced in
+                     place by the number of appended tokens
+        c_t, k_rope: (batch, tokens, dc) and (batch, tokens, dR), one dtype;
+                     k_rope un-rotated (keys are rotated by position inside
+                     the attention)
+        q_rope:      optional (batch * queries_per_seq, num_heads, dR) fp32,
+                     rotated in place for the positions of the last
+                     queries_per_seq appended tokens (needs rope_cos/sin)
+        status:      optional int32 device tensor; element 0 is set to 1 when
+                     a sequence has no room (that sequence is left unchanged)
+    """
+    _C = _load_ext()
+    _C.append_kv_forward(kv_cache, seq_lens, c_t, k_rope, q_rope, rope_cos, rope_sin, seq_offsets, status,
+                         *_cfg_args(cfg))
 
 
 def absorb_q(q_nope: torch.Tensor, W_UK: torch.Tensor, cfg: "MLAConfig") -> torch.Tensor:

@@ -27,6 +27,14 @@ float32). Each function cites the reference code it restates:
   the sequence.
 * ``split_lse_partials`` / ``lse_combine`` -- split-KV partials and their
   log-sum-exp merge (no reference counterpart; pinned by split invariance).
+* ``append_rows``        -- /root/reference/src/mla_config.cuh:57-72
+  (``LatentKVCache::append_host``: row current_len receives [c_t | k_rope],
+  k_rope un-rotated; a full cache is refused), per sequence of a batch with
+  capacity regions.
+* ``rotate_queries``     -- rotate-half RoPE of q_rope (the pairing of
+  /root/reference/src/fused_mla.cu:43-51 and tests/test_python.py:50-54) at
+  the position of the token each query belongs to; the reference itself never
+  rotates the query, so this pins the build's own addition.
 
 Packed cache row layout: [c_t (d_c) | k_rope (d_R)]
 (/root/reference/src/mla_config.cuh:25-28,43-48).
@@ -266,6 +274,49 @@ def lse_combine(parts):
     L = np.logaddexp.reduce(lses, axis=0)
     w = np.exp(lses - L[None, :])
     return np.einsum("sh,shc->hc", w, accs), L
+
+
+# ----------------------------------------------------------------------------
+# cache append and query RoPE
+# ----------------------------------------------------------------------------
+
+def append_rows(kv, starts, caps, lens, c_t, k_rope, cache_dtype: str):
+    """Append tokens to every sequence of a capacity cache.
+
+    kv (rows, dc+dR) float; sequence b owns rows [starts[b], starts[b] +
+    caps[b]) with its first lens[b] filled; c_t (B, T, dc), k_rope (B, T, dR).
+    Following LatentKVCache::append_host (src/mla_config.cuh:57-72), token t
+    lands in row starts[b] + lens[b] + t as [c_t | k_rope] (rounded to the
+    cache dtype, k_rope not rotated) and the length advances; a sequence
+    without room for all T tokens is left unchanged and reported.
+    Returns (kv', lens', full) with full True when any sequence had no room.
+    """
+    kv = np.array(kv, copy=True)
+    lens = np.array(lens, dtype=np.int64, copy=True)
+    T = c_t.shape[1]
+    full = False
+    for b in range(len(lens)):
+        if lens[b] < 0 or lens[b] + T > caps[b]:
+            full = True
+            continue
+        r0 = int(starts[b] + lens[b])
+        kv[r0:r0 + T] = round_to(np.concatenate([c_t[b], k_rope[b]], axis=-1).astype(np.float32), cache_dtype)
+        lens[b] += T
+    return kv, lens, full
+
+
+def rotate_queries(q_rope, lens_old, tokens: int, qps: int, cos, sin):
+    """q_rope (B*qps, nh, dR) rotated for its token's position: query j of
+    sequence b belongs to the token at lens_old[b] + tokens - qps + j
+    (positions past the table use its last row). Rotate-half pairing of
+    src/fused_mla.cu:43-51."""
+    q = np.array(q_rope, dtype=np.float64, copy=True)
+    B = len(lens_old)
+    for b in range(B):
+        for j in range(qps):
+            pos = min(int(lens_old[b]) + tokens - qps + j, cos.shape[0] - 1)
+            q[b * qps + j] = rope_rotate(q[b * qps + j], cos[pos].astype(np.float64), sin[pos].astype(np.float64))
+    return q
 
 
 # ----------------------------------------------------------------------------

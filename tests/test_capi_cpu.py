@@ -20,10 +20,91 @@ from latent_attn import functional as F
 def test_library_exports_header_symbols():
     lib = capi.load()
     names = capi.header_symbols()
-    assert {"la_mla_decode", "la_fused_mla", "la_batched_fused_mla", "la_absorb_q"} <= set(names)
+    assert {"la_mla_decode", "la_fused_mla", "la_batched_fused_mla", "la_absorb_q", "la_append_kv"} <= set(names)
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.la_abi_version() == 2
+    assert lib.la_abi_version() == 3
+
+
+def test_ctypes_structs_match_the_header(tmp_path):
+    """The ctypes mirrors of la_decode_args / la_append_args have the C
+    header's size and field offsets (a C program compiled with gcc prints
+    them)."""
+    import os
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    structs = {"la_decode_args": capi.DecodeArgs, "la_append_args": capi.AppendArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "latent_attn.h"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in py._fields_:
+            lines.append(f'  printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-I" + os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    got = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    want = []
+    for cname, py in structs.items():
+        want.append(f"{cname} size {ctypes.sizeof(py)}")
+        want += [f"{cname} {f} {getattr(py, f).offset}" for f, _ in py._fields_]
+    assert [l for l in got if l] == want
+
+
+def _append_args(**kw):
+    a = capi.AppendArgs()
+    a.cfg = capi.config(MLAConfig.deepseek_v2())
+    a.kv_dtype = capi.LA_DTYPE_BF16
+    a.src_dtype = capi.LA_DTYPE_F32
+    a.num_seqs = 2
+    a.seq_capacity = 8
+    a.total_rows = 16
+    a.tokens_per_seq = 1
+    fake = 0x1000
+    a.kv_cache = a.seq_lens = a.c_t = a.k_rope = fake
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("field,value", [
+    ("num_seqs", -1),
+    ("tokens_per_seq", -1),
+    ("seq_capacity", 9),        # 2 * 9 rows do not fit in total_rows = 16
+    ("kv_dtype", 7),
+    ("src_dtype", 5),
+    ("seq_lens", 0),
+    ("kv_cache", 0),
+    ("c_t", 0),
+    ("k_rope", 0),
+    ("rope_rows", -1),
+    ("q_rope", 0x2000),         # query rotation without tables
+])
+def test_append_rejects_bad_arguments(field, value):
+    lib = capi.load()
+    a = _append_args(**{field: value})
+    assert lib.la_append_kv(ctypes.byref(a), None) == capi.LA_ERROR_INVALID_VALUE
+
+
+def test_append_rejects_more_queries_than_tokens():
+    lib = capi.load()
+    a = _append_args(q_rope=0x2000, rope_cos=0x3000, rope_sin=0x3000, queries_per_seq=2)
+    assert lib.la_append_kv(ctypes.byref(a), None) == capi.LA_ERROR_INVALID_VALUE
+    a = _append_args(q_rope=0x2000, rope_cos=0x3000, rope_sin=0x3000, queries_per_seq=0)
+    assert lib.la_append_kv(ctypes.byref(a), None) == capi.LA_ERROR_INVALID_VALUE
+    assert lib.la_append_kv(None, None) == capi.LA_ERROR_INVALID_VALUE
+
+
+def test_append_empty_batch_is_a_no_op():
+    lib = capi.load()
+    a = _append_args(num_seqs=0, total_rows=0, kv_cache=0, seq_lens=0)
+    assert lib.la_append_kv(ctypes.byref(a), None) == capi.LA_SUCCESS
 
 
 def test_status_strings():

@@ -311,3 +311,61 @@ def test_ragged_sequences_use_in_sequence_positions():
         sl = inp["kv_cache"][offs[b]:offs[b + 1]]
         ref = mo.absorbed_mla(sl, qa[b], inp["q_rope"][b], inp["W_UV"], cos, sin, cfg)
         assert np.allclose(out[b], ref, rtol=1e-12, atol=1e-14)
+
+
+# ---- cache append and query RoPE (device-side append_host) ----------------
+
+def test_append_rows_places_rows_and_refuses_full():
+    """Rows land at start + length (src/mla_config.cuh:57-72), lengths
+    advance, other rows are untouched, a sequence without room is left as it
+    was and reported; checked against hand-written expectations."""
+    row = 576
+    kv = np.full((12, row), -7.0, dtype=np.float32)
+    starts, caps, lens = [0, 4, 8], [4, 4, 4], [1, 3, 0]
+    c_t = np.arange(3 * 2 * 512, dtype=np.float32).reshape(3, 2, 512)
+    k_rope = -np.arange(3 * 2 * 64, dtype=np.float32).reshape(3, 2, 64)
+    out, new_lens, full = mo.append_rows(kv, starts, caps, lens, c_t, k_rope, "f32")
+    assert full  # sequence 1 has 3 of 4 rows filled: no room for 2
+    assert list(new_lens) == [3, 3, 2]
+    for b, r in ((0, 1), (2, 8)):
+        for t in range(2):
+            assert np.array_equal(out[r + t, :512], c_t[b, t]) and np.array_equal(out[r + t, 512:], k_rope[b, t])
+    untouched = [0, 3, 4, 5, 6, 7, 10, 11]
+    assert np.all(out[untouched] == -7.0)
+
+
+def test_append_rows_rounds_to_the_cache_dtype():
+    kv = np.zeros((2, 576), dtype=np.float32)
+    c_t = np.full((1, 1, 512), 1.0 + 2.0 ** -9, dtype=np.float32)  # halfway between two bf16 values
+    k_rope = np.full((1, 1, 64), 3.0 + 2.0 ** -7, dtype=np.float32)
+    out, _, _ = mo.append_rows(kv, [0], [2], [0], c_t, k_rope, "bf16")
+    assert out[0, 0] == 1.0            # ties go to the even mantissa
+    assert out[0, 512] == 3.0 + 2.0 ** -6 or out[0, 512] == 3.0
+    assert np.array_equal(out[0, 512:], mo.bf16_round(k_rope[0, 0]))
+
+
+def test_rotate_queries_closed_form():
+    """A one-hot q_rope e_i at position p rotates to cos(p w_i) e_i +
+    sin(p w_i) e_{i+32}, w_i = 10000^(-2i/64) (textbook 2-D rotation); query
+    j of a sequence with old length L and T appended tokens sits at
+    L + T - qps + j; position 0 is the identity; norms are preserved."""
+    nh, dR, qps, T = 2, 64, 2, 3
+    cos, sin = mo.build_rope_tables(64, dR)
+    lens_old = [5, 0]
+    q = np.zeros((2 * qps, nh, dR))
+    for r in range(2 * qps):
+        q[r, 0, r] = 1.0          # e_r in head 0
+        q[r, 1, :] = np.linspace(-1, 1, dR) * (r + 1)
+    got = mo.rotate_queries(q, lens_old, T, qps, cos, sin)
+    for b in range(2):
+        for j in range(qps):
+            r = b * qps + j
+            pos = lens_old[b] + T - qps + j
+            w = 10000.0 ** (-2.0 * r / dR)
+            expect = np.zeros(dR)
+            expect[r], expect[r + 32] = math.cos(pos * w), math.sin(pos * w)
+            assert np.allclose(got[r, 0], expect, atol=2e-6), (b, j)
+            assert math.isclose(np.linalg.norm(got[r, 1]), np.linalg.norm(q[r, 1]), rel_tol=1e-6)
+    # T == qps with an empty cache: the first query sits at position 0
+    same = mo.rotate_queries(q[:1], [0], 1, 1, cos, sin)
+    assert np.array_equal(same, q[:1])
