@@ -173,35 +173,22 @@ torch::Tensor batched_fused_mla_forward(torch::Tensor kv_cache, torch::Tensor q_
 //   returns (B, nh, dv) f32. chunk_rows / kernel_variant: tuning overrides.
 //   seq_lens: None or int32 (B,) device tensor; sequence b is the first
 //   seq_lens[b] rows of its region (a capacity cache filled by append_kv).
-torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, torch::Tensor q_rope,
-                                 torch::Tensor W_UK, torch::Tensor W_UV, torch::Tensor rope_cos,
-                                 torch::Tensor rope_sin, c10::optional<torch::Tensor> seq_offsets, int d_model,
-                                 int kv_lora_rank, int qk_nope_head_dim, int qk_rope_head_dim, int num_heads,
-                                 int v_head_dim, int chunk_rows, int kernel_variant,
-                                 c10::optional<torch::Tensor> seq_lens) {
-  check_storage(kv_cache, "kv_cache");
-  check_fp32_contiguous(q_nope, "q_nope");
-  check_fp32_contiguous(q_rope, "q_rope");
-  check_storage(W_UK, "W_UK");
-  check_storage(W_UV, "W_UV");
-  check_fp32_contiguous(rope_cos, "rope_cos");
-  check_fp32_contiguous(rope_sin, "rope_sin");
-  la_mla_config cfg =
-      config_from_args(d_model, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, num_heads, v_head_dim);
-  const int64_t row = kv_lora_rank + qk_rope_head_dim;
-  TORCH_CHECK(q_nope.dim() == 3 && q_nope.size(1) == num_heads && q_nope.size(2) == qk_nope_head_dim,
-              "q_nope must be (batch, num_heads, qk_nope_head_dim)");
-  const int64_t batch = q_nope.size(0);
-  TORCH_CHECK(q_rope.dim() == 3 && q_rope.size(0) == batch && q_rope.size(1) == num_heads &&
-                  q_rope.size(2) == qk_rope_head_dim,
-              "q_rope must be (batch, num_heads, qk_rope_head_dim)");
-  TORCH_CHECK(W_UK.dim() == 2 && W_UK.size(0) == (int64_t)num_heads * qk_nope_head_dim && W_UK.size(1) == kv_lora_rank,
-              "W_UK shape mismatch");
-  TORCH_CHECK(W_UV.dim() == 2 && W_UV.size(0) == (int64_t)num_heads * v_head_dim && W_UV.size(1) == kv_lora_rank,
-              "W_UV shape mismatch");
-  TORCH_CHECK(batch <= INT32_MAX / num_heads, "batch too large");
+namespace {
 
-  la_decode_args a{};
+// Shared by mla_decode_forward and mla_decode_absorbed_forward: checks the
+// cache / sequence / table arguments, fills the descriptor and runs it.
+torch::Tensor run_decode(la_decode_args& a, const torch::Tensor& kv_cache, const torch::Tensor& q_rope,
+                         const torch::Tensor& W_UV, const torch::Tensor& rope_cos, const torch::Tensor& rope_sin,
+                         const c10::optional<torch::Tensor>& seq_offsets, const c10::optional<torch::Tensor>& seq_lens,
+                         const la_mla_config& cfg, int64_t batch, int chunk_rows, int kernel_variant) {
+  const int64_t row = cfg.kv_lora_rank + cfg.qk_rope_head_dim;
+  TORCH_CHECK(q_rope.dim() == 3 && q_rope.size(0) == batch && q_rope.size(1) == cfg.num_heads &&
+                  q_rope.size(2) == cfg.qk_rope_head_dim,
+              "q_rope must be (batch, num_heads, qk_rope_head_dim)");
+  TORCH_CHECK(W_UV.dim() == 2 && W_UV.size(0) == (int64_t)cfg.num_heads * cfg.v_head_dim &&
+                  W_UV.size(1) == cfg.kv_lora_rank,
+              "W_UV shape mismatch");
+  TORCH_CHECK(batch <= INT32_MAX / cfg.num_heads, "batch too large");
   a.kv_cache = kv_cache.data_ptr();
   a.kv_dtype = dtype_tag(kv_cache);
   a.num_seqs = (int32_t)batch;
@@ -218,7 +205,6 @@ torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, t
     a.seq_offsets = off.data_ptr<int32_t>();
     // Sequences are at most total_rows long; positions past the table clamp.
     longest = 0;
-    a.rope_rows = rope_cos.size(0);
   } else {
     TORCH_CHECK(kv_cache.dim() == 3 && kv_cache.size(0) == batch && kv_cache.size(2) == row,
                 "kv_cache must be (batch, seq_len, ", row, ") when seq_offsets is None");
@@ -226,8 +212,8 @@ torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, t
     a.seq_len = (int32_t)kv_cache.size(1);
     a.total_rows = batch * kv_cache.size(1);
     longest = kv_cache.size(1);
-    a.rope_rows = rope_cos.size(0);
   }
+  a.rope_rows = rope_cos.size(0);
   if (seq_lens.has_value() && seq_lens->defined()) {
     const auto& len = *seq_lens;
     TORCH_CHECK(len.dtype() == torch::kInt32 && len.is_contiguous() && len.is_cuda(),
@@ -238,10 +224,7 @@ torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, t
     longest = 0;  // lengths live on the device; positions past the table clamp
   }
   check_rope(rope_cos, rope_sin, longest, cfg);
-  for (auto* t : {&q_nope, &q_rope, &W_UK, &W_UV, &rope_cos, &rope_sin}) check_same_device(kv_cache, *t, "inputs");
-  a.q_nope = q_nope.data_ptr<float>();
-  a.W_UK = W_UK.data_ptr();
-  a.w_uk_dtype = dtype_tag(W_UK);
+  for (auto* t : {&q_rope, &W_UV, &rope_cos, &rope_sin}) check_same_device(kv_cache, *t, "inputs");
   a.q_rope = q_rope.data_ptr<float>();
   a.W_UV = W_UV.data_ptr();
   a.w_uv_dtype = dtype_tag(W_UV);
@@ -252,7 +235,7 @@ torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, t
   a.kernel_variant = kernel_variant;
 
   const at::DeviceGuard guard(kv_cache.device());
-  auto output = torch::empty({batch, num_heads, v_head_dim}, kv_cache.options().dtype(torch::kFloat32));
+  auto output = torch::empty({batch, cfg.num_heads, cfg.v_head_dim}, kv_cache.options().dtype(torch::kFloat32));
   a.output = output.data_ptr<float>();
   const size_t ws_bytes = la_mla_decode_workspace_size(&a);
   TORCH_CHECK(ws_bytes > 0 || batch == 0, "mla_decode: unsupported arguments");
@@ -261,6 +244,62 @@ torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, t
   a.workspace_bytes = ws_bytes;
   check_status(la_mla_decode(&a, current_stream()), "la_mla_decode");
   return output;
+}
+
+}  // namespace
+
+torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, torch::Tensor q_rope,
+                                 torch::Tensor W_UK, torch::Tensor W_UV, torch::Tensor rope_cos,
+                                 torch::Tensor rope_sin, c10::optional<torch::Tensor> seq_offsets, int d_model,
+                                 int kv_lora_rank, int qk_nope_head_dim, int qk_rope_head_dim, int num_heads,
+                                 int v_head_dim, int chunk_rows, int kernel_variant,
+                                 c10::optional<torch::Tensor> seq_lens) {
+  check_storage(kv_cache, "kv_cache");
+  check_fp32_contiguous(q_nope, "q_nope");
+  check_fp32_contiguous(q_rope, "q_rope");
+  check_storage(W_UK, "W_UK");
+  check_storage(W_UV, "W_UV");
+  check_fp32_contiguous(rope_cos, "rope_cos");
+  check_fp32_contiguous(rope_sin, "rope_sin");
+  la_mla_config cfg =
+      config_from_args(d_model, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, num_heads, v_head_dim);
+  TORCH_CHECK(q_nope.dim() == 3 && q_nope.size(1) == num_heads && q_nope.size(2) == qk_nope_head_dim,
+              "q_nope must be (batch, num_heads, qk_nope_head_dim)");
+  TORCH_CHECK(W_UK.dim() == 2 && W_UK.size(0) == (int64_t)num_heads * qk_nope_head_dim && W_UK.size(1) == kv_lora_rank,
+              "W_UK shape mismatch");
+  check_same_device(kv_cache, q_nope, "q_nope");
+  check_same_device(kv_cache, W_UK, "W_UK");
+  la_decode_args a{};
+  a.q_nope = q_nope.data_ptr<float>();
+  a.W_UK = W_UK.data_ptr();
+  a.w_uk_dtype = dtype_tag(W_UK);
+  return run_decode(a, kv_cache, q_rope, W_UV, rope_cos, rope_sin, seq_offsets, seq_lens, cfg, q_nope.size(0),
+                    chunk_rows, kernel_variant);
+}
+
+// mla_decode_absorbed_forward -- the same step for queries already absorbed
+// (q_absorbed (B, nh, dc) f32, e.g. x . W_Q_absorbed^T as the reference's
+// LatentAttentionLayer computes them, latent_attn/__init__.py:124-126).
+torch::Tensor mla_decode_absorbed_forward(torch::Tensor kv_cache, torch::Tensor q_absorbed, torch::Tensor q_rope,
+                                          torch::Tensor W_UV, torch::Tensor rope_cos, torch::Tensor rope_sin,
+                                          c10::optional<torch::Tensor> seq_offsets, int d_model, int kv_lora_rank,
+                                          int qk_nope_head_dim, int qk_rope_head_dim, int num_heads, int v_head_dim,
+                                          int chunk_rows, int kernel_variant, c10::optional<torch::Tensor> seq_lens) {
+  check_storage(kv_cache, "kv_cache");
+  check_fp32_contiguous(q_absorbed, "q_absorbed");
+  check_fp32_contiguous(q_rope, "q_rope");
+  check_storage(W_UV, "W_UV");
+  check_fp32_contiguous(rope_cos, "rope_cos");
+  check_fp32_contiguous(rope_sin, "rope_sin");
+  la_mla_config cfg =
+      config_from_args(d_model, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, num_heads, v_head_dim);
+  TORCH_CHECK(q_absorbed.dim() == 3 && q_absorbed.size(1) == num_heads && q_absorbed.size(2) == kv_lora_rank,
+              "q_absorbed must be (batch, num_heads, kv_lora_rank)");
+  check_same_device(kv_cache, q_absorbed, "q_absorbed");
+  la_decode_args a{};
+  a.q_absorbed = q_absorbed.data_ptr<float>();
+  return run_decode(a, kv_cache, q_rope, W_UV, rope_cos, rope_sin, seq_offsets, seq_lens, cfg, q_absorbed.size(0),
+                    chunk_rows, kernel_variant);
 }
 
 // append_kv_forward -- device-side LatentKVCache::append_host
@@ -421,6 +460,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("kv_lora_rank"), py::arg("qk_nope_head_dim"), py::arg("qk_rope_head_dim"), py::arg("num_heads"),
         py::arg("v_head_dim"), py::arg("chunk_rows") = 0, py::arg("kernel_variant") = 0,
         py::arg("seq_lens") = py::none());
+  m.def("mla_decode_absorbed_forward", &mla_decode_absorbed_forward,
+        "Batched MLA decode step for pre-absorbed queries (split-KV, combine, W_UV)", py::arg("kv_cache"),
+        py::arg("q_absorbed"), py::arg("q_rope"), py::arg("W_UV"), py::arg("rope_cos"), py::arg("rope_sin"),
+        py::arg("seq_offsets"), py::arg("d_model"), py::arg("kv_lora_rank"), py::arg("qk_nope_head_dim"),
+        py::arg("qk_rope_head_dim"), py::arg("num_heads"), py::arg("v_head_dim"), py::arg("chunk_rows") = 0,
+        py::arg("kernel_variant") = 0, py::arg("seq_lens") = py::none());
   m.def("append_kv_forward", &append_kv_forward,
         "Device-side append of latent rows at each sequence's length, with the query's RoPE",
         py::arg("kv_cache"), py::arg("seq_lens"), py::arg("c_t"), py::arg("k_rope"), py::arg("q_rope"),

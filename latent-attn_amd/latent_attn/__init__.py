@@ -12,7 +12,7 @@ from dataclasses import dataclass
 
 import torch
 
-__all__ = ["MLAConfig", "build_rope_tables", "_build_rope_tables"]
+__all__ = ["MLAConfig", "LatentAttentionLayer", "build_rope_tables", "_build_rope_tables"]
 
 
 @dataclass
@@ -65,3 +65,6 @@ def build_rope_tables(seq_len: int, d_R: int, device=None, base: float = 10000.0
 
 def _build_rope_tables(seq_len: int, d_R: int, device: torch.device):
     return build_rope_tables(seq_len, d_R, device)
+
+
+from .layer import LatentAttentionLayer  # noqa: E402  (needs MLAConfig and build_rope_tables above)

@@ -146,6 +146,27 @@ def mla_decode(
                                  *_cfg_args(cfg), chunk_rows, kernel_variant, seq_lens)
 
 
+def mla_decode_absorbed(
+    kv_cache: torch.Tensor,
+    q_absorbed: torch.Tensor,
+    q_rope: torch.Tensor,
+    W_UV: torch.Tensor,
+    rope_cos: torch.Tensor,
+    rope_sin: torch.Tensor,
+    cfg: "MLAConfig",
+    seq_offsets: Optional[torch.Tensor] = None,
+    seq_lens: Optional[torch.Tensor] = None,
+    chunk_rows: int = 0,
+    kernel_variant: int = 0,
+) -> torch.Tensor:
+    """``mla_decode`` for queries already in latent space: q_absorbed
+    (batch, num_heads, kv_lora_rank) fp32 (e.g. x . W_Q_absorbed^T). Same
+    cache / sequence arguments; returns (batch, num_heads, v_head_dim) fp32."""
+    _C = _load_ext()
+    return _C.mla_decode_absorbed_forward(kv_cache, q_absorbed, q_rope, W_UV, rope_cos, rope_sin, seq_offsets,
+                                          *_cfg_args(cfg), chunk_rows, kernel_variant, seq_lens)
+
+
 def append_kv(
     kv_cache: torch.Tensor,
     seq_lens: torch.Tensor,

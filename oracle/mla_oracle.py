@@ -31,6 +31,10 @@ float32). Each function cites the reference code it restates:
   (``LatentKVCache::append_host``: row current_len receives [c_t | k_rope],
   k_rope un-rotated; a full cache is refused), per sequence of a batch with
   capacity regions.
+* ``layer_forward``      -- /root/reference/latent_attn/__init__.py:110-145
+  (``LatentAttentionLayer.forward``): q_abs = W_Q_absorbed x, q_rope =
+  W_Q_rope x (not rotated), the absorbed attention with W_UV rounded to fp16
+  (``_w_uv_fp16``, :98-99), then W_O over the flattened heads.
 * ``rotate_queries``     -- rotate-half RoPE of q_rope (the pairing of
   /root/reference/src/fused_mla.cu:43-51 and tests/test_python.py:50-54) at
   the position of the token each query belongs to; the reference itself never
@@ -274,6 +278,20 @@ def lse_combine(parts):
     L = np.logaddexp.reduce(lses, axis=0)
     w = np.exp(lses - L[None, :])
     return np.einsum("sh,shc->hc", w, accs), L
+
+
+def layer_forward(x, kv_cache, W_Q_absorbed, W_Q_rope, W_UV, W_O, rope_cos, rope_sin, cfg: Dims,
+                  dtype=np.float64):
+    """LatentAttentionLayer.forward (latent_attn/__init__.py:110-145) for one
+    token x (d_model,) over kv_cache (S, dc+dR): returns (d_model,)."""
+    nh, dc, dR = cfg.num_heads, cfg.kv_lora_rank, cfg.qk_rope_head_dim
+    x = np.asarray(x, dtype=dtype)
+    q_abs = (np.asarray(W_Q_absorbed, dtype=dtype) @ x).reshape(nh, dc)
+    q_r = (np.asarray(W_Q_rope, dtype=dtype) @ x).reshape(nh, dR)
+    S = kv_cache.shape[0]
+    out = absorbed_mla(kv_cache, q_abs, q_r, f16_round(np.asarray(W_UV, dtype=np.float32)), rope_cos[:S],
+                       rope_sin[:S], cfg, dtype)
+    return np.asarray(W_O, dtype=dtype) @ out.reshape(-1)
 
 
 # ----------------------------------------------------------------------------

@@ -369,3 +369,49 @@ def test_rotate_queries_closed_form():
     # T == qps with an empty cache: the first query sits at position 0
     same = mo.rotate_queries(q[:1], [0], 1, 1, cos, sin)
     assert np.array_equal(same, q[:1])
+
+
+# ---- LatentAttentionLayer.forward ---------------------------------------
+
+def _layer_case(seed=3, d_model=96, nh=4, S=20):
+    cfg = mo.Dims(d_model, 16, 8, 8, nh, 12)
+    rs = np.random.RandomState(seed)
+    p = dict(W_Q_absorbed=rs.standard_normal((nh * 16, d_model)) * 0.02,
+             W_Q_rope=rs.standard_normal((nh * 8, d_model)) * 0.02,
+             W_UV=rs.standard_normal((nh * 12, 16)) * 0.3,
+             W_O=rs.standard_normal((d_model, nh * 12)) * 0.02)
+    kv = rs.standard_normal((S, 24))
+    cos, sin = mo.build_rope_tables(S, 8)
+    return cfg, p, kv, cos, sin, rs
+
+
+def test_layer_forward_zero_token_is_projected_mean():
+    """x = 0 gives q = 0, uniform attention weights, so y = W_O . concat_h(
+    W_UV_h . mean(c_t)) with W_UV rounded to fp16 (_w_uv_fp16,
+    latent_attn/__init__.py:98-99): computed here from means and per-head
+    products only."""
+    cfg, p, kv, cos, sin, _ = _layer_case()
+    y = mo.layer_forward(np.zeros(cfg.d_model), kv, p["W_Q_absorbed"], p["W_Q_rope"], p["W_UV"], p["W_O"], cos, sin,
+                         cfg)
+    mean_c = kv[:, :16].mean(axis=0)
+    W_UV16 = mo.f16_round(p["W_UV"]).astype(np.float64)
+    heads = np.concatenate([W_UV16[h * 12:(h + 1) * 12] @ mean_c for h in range(cfg.num_heads)])
+    assert np.allclose(y, p["W_O"] @ heads, rtol=1e-12, atol=1e-14)
+    # the fp16 rounding of W_UV is part of the path: unrounded weights differ
+    assert not np.allclose(y, p["W_O"] @ np.concatenate(
+        [p["W_UV"][h * 12:(h + 1) * 12] @ mean_c for h in range(cfg.num_heads)]), rtol=1e-9, atol=0)
+
+
+def test_layer_forward_is_linear_in_w_o_and_uses_unrotated_queries():
+    """y is linear in W_O; the query projections enter the attention as they
+    are (the reference never rotates q): the result equals absorbed_mla on
+    (W_Q_absorbed x, W_Q_rope x)."""
+    cfg, p, kv, cos, sin, rs = _layer_case(seed=4)
+    x = rs.standard_normal(cfg.d_model)
+    y1 = mo.layer_forward(x, kv, p["W_Q_absorbed"], p["W_Q_rope"], p["W_UV"], p["W_O"], cos, sin, cfg)
+    y2 = mo.layer_forward(x, kv, p["W_Q_absorbed"], p["W_Q_rope"], p["W_UV"], 2.5 * p["W_O"], cos, sin, cfg)
+    assert np.allclose(y2, 2.5 * y1, rtol=1e-12, atol=1e-15)
+    qa = (p["W_Q_absorbed"] @ x).reshape(4, 16)
+    qr = (p["W_Q_rope"] @ x).reshape(4, 8)
+    out = mo.absorbed_mla(kv, qa, qr, mo.f16_round(p["W_UV"]), cos, sin, cfg)
+    assert np.allclose(y1, p["W_O"] @ out.reshape(-1), rtol=1e-12, atol=1e-15)
