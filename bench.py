@@ -197,6 +197,40 @@ def time_append(lib, hip, capi, inp, stream, calls: int = 100) -> float:
     return us
 
 
+def time_layer(hip, inp, stream, calls: int = 20) -> dict:
+    """LatentAttentionLayer.forward_batch (DeepSeek-V2 dims, fp32 parameters
+    as in the reference module) for one token per sequence over the
+    workload's cache: microseconds per call over `calls` calls between one
+    event pair, against the HBM time of its algorithmic bytes (fp32 weights
+    W_Q_absorbed, W_Q_rope, W_O, fp16 W_UV, the latent cache)."""
+    import torch
+
+    from latent_attn import LatentAttentionLayer
+
+    cfg, B = inp["cfg"], inp["B"]
+    dev = inp["kv"].device
+    torch.manual_seed(0)
+    layer = LatentAttentionLayer(cfg, max_seq_len=inp["max_len"]).to(dev)
+    x = torch.randn(B, cfg.d_model, device=dev)
+    kv = inp["kv"] if inp["offsets"] is not None else inp["kv"].view(B, inp["seq_len"], -1)
+    run = lambda: layer.forward_batch(x, kv, seq_offsets=inp["offsets"])
+    for _ in range(3):
+        run()
+    t0, t1 = new_event(hip), new_event(hip)
+    torch.cuda.synchronize()
+    hip.hipEventRecord(t0, ctypes.c_void_p(stream))
+    for _ in range(calls):
+        run()
+    hip.hipEventRecord(t1, ctypes.c_void_p(stream))
+    hip.hipEventSynchronize(t1)
+    us = elapsed_ms(hip, t0, t1) * 1e3 / calls
+    hip.hipEventDestroy(t0)
+    hip.hipEventDestroy(t1)
+    wbytes = 4 * (layer.W_Q_absorbed.numel() + layer.W_Q_rope.numel() + layer.W_O.numel()) + 2 * layer.W_UV.numel()
+    total = wbytes + int(inp["total"]) * BYTES_PER_POS
+    return {"us": round(us, 1), "algorithmic_bytes": total, "hbm_frac": round(total / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
 def measured_traffic(config: str):
     """HBM bytes per attention-kernel launch measured with rocprofv3
     (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size), read from the
@@ -266,6 +300,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--layer", action="store_true",
+                    help="also time LatentAttentionLayer.forward_batch (fp32 projections, 1.8 GB of weights) "
+                         "on the same batch and cache")
     ap.add_argument("--variant", type=int, default=0, help="0 auto, 1 VALU kernel, 2 MFMA kernel")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 3 device-to-device copies of MIB MiB (the known-size kernel that scales "
@@ -352,6 +389,7 @@ def main():
     ms_step = ms_total / K
     us_step = ms_step * 1e3
     append_us = time_append(lib, hip, capi, inp, stream)
+    layer = time_layer(hip, inp, stream) if args.layer else None
 
     total_pos = int(inp["total"])
     cache_bytes = total_pos * BYTES_PER_POS
@@ -388,6 +426,7 @@ def main():
         "attn_kernel_us_min_max": [round(kern_ms[0] * 1e3, 2), round(kern_ms[-1] * 1e3, 2)],
         "mfma_frac_of_bf16_peak": round(flops_attn / (kern_avg * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         "append_kernel_us": round(append_us, 2),
+        **({"layer_forward_batch": layer} if layer else {}),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved_gbps, 1),
