@@ -12,6 +12,8 @@
  *                            src/fused_mla.cu:271-296
  *   la_batched_fused_mla  <- launch_batched_fused_mla  src/fused_mla_batched.cuh:35,
  *                            src/fused_mla_batched.cu:109-130
+ *   la_naive_mla          <- naive_mla_forward         csrc/bindings.cpp:53-114,
+ *                            src/naive_mla.cu:91-245 (decompress-then-attend)
  *   la_absorb_q           <- host absorption loop tests/test_correctness.cu:29-46
  *                            and einsum tests/test_python.py:97-99
  *   la_mla_decode         <- the decode step the north star adds on top of the
@@ -218,6 +220,22 @@ int la_batched_fused_mla(const void* kv_cache, int kv_dtype, int seq_len, int ba
 /* Workspace bytes la_fused_mla / la_batched_fused_mla need (batch_size 1 for
  * la_fused_mla). */
 size_t la_fused_mla_workspace_size(int seq_len, int batch_size, const la_mla_config* cfg);
+
+/* Decompress-then-attend on the GPU, the reference's naive path
+ * (naive_mla_forward, csrc/bindings.cpp:53-114; math of
+ * tests/test_python.py:26-63): K_nope = c_t W_UK^T, V = c_t W_UV^T, RoPE on
+ * k_rope, softmax, P V, all fp32, computed independently of the absorbed
+ * kernels (a GPU check for shapes where a CPU restatement is slow). One query:
+ * q_nope (num_heads, qk_nope_head_dim), q_rope (num_heads, qk_rope_head_dim)
+ * f32 (already rotated); output (num_heads, v_head_dim) f32; rope tables have
+ * >= seq_len rows. Workspace: la_naive_mla_workspace_size bytes (fp32 K_nope,
+ * V and scores), or NULL for a stream-ordered allocation. The reference's
+ * cuBLAS call reads K/V transposed (its naive path is wrong); this one is not. */
+int la_naive_mla(const void* kv_cache, int kv_dtype, int seq_len, const void* W_UK, int w_uk_dtype, const void* W_UV,
+                 int w_uv_dtype, const float* q_nope, const float* q_rope, const float* rope_cos,
+                 const float* rope_sin, float* output, const la_mla_config* cfg, void* workspace,
+                 size_t workspace_bytes, void* stream);
+size_t la_naive_mla_workspace_size(int seq_len, const la_mla_config* cfg);
 
 /* Appends tokens_per_seq rows to every sequence's cache on the device and
  * advances seq_lens (replaces LatentKVCache::append_host,

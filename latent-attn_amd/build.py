@@ -28,7 +28,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
 LIB_NAME = "liblatent_attn_hip.so"
-HIP_SOURCES = ["la_append.hip", "la_capi.hip", "la_generic.hip", "la_mfma.hip", "la_proj.hip"]
+HIP_SOURCES = ["la_append.hip", "la_capi.hip", "la_generic.hip", "la_mfma.hip", "la_naive.hip", "la_proj.hip"]
 
 # -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32.
 HIP_FLAGS = [

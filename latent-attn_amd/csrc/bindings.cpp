@@ -419,10 +419,9 @@ torch::Tensor absorb_q_forward(torch::Tensor q_nope, torch::Tensor W_UK, int d_m
   return out;
 }
 
-// naive_mla_forward -- reference csrc/bindings.cpp:53-114 signature. The
-// result is the same function of the inputs (decompress-then-attend equals
-// absorb-then-attend); it is computed by absorbing q_nope with W_UK on the GPU
-// and running the fused decode, so no (S, nh*dn) K/V is materialised.
+// naive_mla_forward -- reference csrc/bindings.cpp:53-114 signature:
+// decompress-then-attend on the GPU (la_naive_mla: K_nope and V materialised
+// in fp32, RoPE, softmax, P V), independent of the absorbed kernels.
 torch::Tensor naive_mla_forward(torch::Tensor kv_cache, torch::Tensor W_UK, torch::Tensor W_UV,
                                 torch::Tensor q_nope, torch::Tensor q_rope, torch::Tensor rope_cos,
                                 torch::Tensor rope_sin, int d_model, int kv_lora_rank, int qk_nope_head_dim,
@@ -441,10 +440,26 @@ torch::Tensor naive_mla_forward(torch::Tensor kv_cache, torch::Tensor W_UK, torc
               "q_nope shape mismatch");
   TORCH_CHECK(q_rope.dim() == 2 && q_rope.size(0) == num_heads && q_rope.size(1) == qk_rope_head_dim,
               "q_rope shape mismatch");
-  auto out = mla_decode_forward(kv_cache.unsqueeze(0), q_nope.unsqueeze(0), q_rope.unsqueeze(0), W_UK, W_UV,
-                                rope_cos, rope_sin, c10::nullopt, d_model, kv_lora_rank, qk_nope_head_dim,
-                                qk_rope_head_dim, num_heads, v_head_dim, 0, 0, c10::nullopt);
-  return out.squeeze(0);
+  TORCH_CHECK(W_UK.dim() == 2 && W_UK.size(0) == (int64_t)num_heads * qk_nope_head_dim && W_UK.size(1) == kv_lora_rank,
+              "W_UK shape mismatch");
+  TORCH_CHECK(W_UV.dim() == 2 && W_UV.size(0) == (int64_t)num_heads * v_head_dim && W_UV.size(1) == kv_lora_rank,
+              "W_UV shape mismatch");
+  TORCH_CHECK(kv_cache.size(0) <= INT32_MAX, "seq_len too large");
+  const int seq_len = (int)kv_cache.size(0);
+  la_mla_config cfg =
+      config_from_args(d_model, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, num_heads, v_head_dim);
+  check_rope(rope_cos, rope_sin, seq_len, cfg);
+  for (auto* t : {&W_UK, &W_UV, &q_nope, &q_rope, &rope_cos, &rope_sin}) check_same_device(kv_cache, *t, "inputs");
+  const at::DeviceGuard guard(kv_cache.device());
+  auto out = torch::empty({num_heads, v_head_dim}, kv_cache.options().dtype(torch::kFloat32));
+  const size_t ws_bytes = la_naive_mla_workspace_size(seq_len, &cfg);
+  auto ws = workspace(kv_cache, ws_bytes);
+  check_status(la_naive_mla(kv_cache.data_ptr(), dtype_tag(kv_cache), seq_len, W_UK.data_ptr(), dtype_tag(W_UK),
+                            W_UV.data_ptr(), dtype_tag(W_UV), q_nope.data_ptr<float>(), q_rope.data_ptr<float>(),
+                            rope_cos.data_ptr<float>(), rope_sin.data_ptr<float>(), out.data_ptr<float>(), &cfg,
+                            ws.data_ptr(), ws_bytes, current_stream()),
+               "la_naive_mla");
+  return out;
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {

@@ -353,6 +353,59 @@ size_t la_fused_mla_workspace_size(int seq_len, int batch_size, const la_mla_con
   return best;
 }
 
+size_t la_naive_mla_workspace_size(int seq_len, const la_mla_config* cfg) {
+  if (!la::valid_cfg(cfg) || seq_len < 0) return 0;
+  return la::naive_workspace_bytes(seq_len, cfg->num_heads, cfg->qk_nope_head_dim, cfg->v_head_dim);
+}
+
+int la_naive_mla(const void* kv_cache, int kv_dtype, int seq_len, const void* W_UK, int w_uk_dtype, const void* W_UV,
+                 int w_uv_dtype, const float* q_nope, const float* q_rope, const float* rope_cos,
+                 const float* rope_sin, float* output, const la_mla_config* cfg, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  if (!la::valid_cfg(cfg) || seq_len < 0 || !la::valid_dtype(kv_dtype) || !la::valid_dtype(w_uk_dtype) ||
+      !la::valid_dtype(w_uv_dtype))
+    return LA_ERROR_INVALID_VALUE;
+  if (!W_UK || !W_UV || !q_nope || !q_rope || !rope_cos || !rope_sin || !output || (seq_len > 0 && !kv_cache))
+    return LA_ERROR_INVALID_VALUE;
+  const size_t need = la::naive_workspace_bytes(seq_len, cfg->num_heads, cfg->qk_nope_head_dim, cfg->v_head_dim);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  la::NaiveProblem p{};
+  p.kv = kv_cache;
+  p.kv_dtype = kv_dtype;
+  p.S = seq_len;
+  p.W_UK = W_UK;
+  p.wuk_dtype = w_uk_dtype;
+  p.W_UV = W_UV;
+  p.wuv_dtype = w_uv_dtype;
+  p.q_nope = q_nope;
+  p.q_rope = q_rope;
+  p.rope_cos = rope_cos;
+  p.rope_sin = rope_sin;
+  p.rope_rows = seq_len;  // the reference indexes cos/sin by position < seq_len (src/fused_mla.cu:158-159)
+  p.out = output;
+  p.nh = cfg->num_heads;
+  p.dn = cfg->qk_nope_head_dim;
+  p.dR = cfg->qk_rope_head_dim;
+  p.dc = cfg->kv_lora_rank;
+  p.dv = cfg->v_head_dim;
+  p.scale = (float)(1.0 / std::sqrt((double)(cfg->qk_nope_head_dim + cfg->qk_rope_head_dim)));
+  void* ws = workspace;
+  bool owned = false;
+  if (ws) {
+    if (workspace_bytes < need) return LA_ERROR_WORKSPACE;
+  } else if (need > 0) {
+    hipError_t e = hipMallocAsync(&ws, need, st);
+    if (e != hipSuccess) return la::record_hip(e);
+    owned = true;
+  }
+  hipError_t e = la::launch_naive(p, ws, st);
+  if (owned) {
+    hipError_t f = hipFreeAsync(ws, st);
+    if (e == hipSuccess) e = f;
+  }
+  return e == hipSuccess ? (int)LA_SUCCESS : la::record_hip(e);
+}
+
 int la_append_kv(const la_append_args* a, void* stream) {
   if (!a || !la::valid_cfg(&a->cfg) || !la::valid_dtype(a->kv_dtype) || !la::valid_dtype(a->src_dtype))
     return LA_ERROR_INVALID_VALUE;

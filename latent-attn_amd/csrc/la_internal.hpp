@@ -177,7 +177,33 @@ struct AppendProblem {
   int dc, dR;
 };
 
+// One la_naive_mla call (la_naive.hip): a single query over one cache.
+struct NaiveProblem {
+  const void* kv;
+  int kv_dtype;
+  int S;
+  const void* W_UK;
+  int wuk_dtype;
+  const void* W_UV;
+  int wuv_dtype;
+  const float* q_nope;
+  const float* q_rope;
+  const float* rope_cos;
+  const float* rope_sin;
+  int64_t rope_rows;
+  float* out;
+  int nh, dn, dR, dc, dv;
+  float scale;
+  float* Kn;      // workspace: (S, nh*dn) fp32
+  float* V;       // workspace: (S, nh*dv) fp32
+  float* scores;  // workspace: (nh, S) fp32
+};
+
 // ---- host launchers (one per kernel family) -------------------------------
+
+// Decompress-then-attend (la_naive.hip).
+size_t naive_workspace_bytes(int64_t S, int nh, int dn, int dv);
+hipError_t launch_naive(NaiveProblem p, void* workspace, hipStream_t stream);
 
 // Device-side cache append + query RoPE.
 hipError_t launch_append(const AppendProblem& p, hipStream_t stream);

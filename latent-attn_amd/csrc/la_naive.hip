@@ -1,0 +1,190 @@
+// Decompress-then-attend MLA on the GPU (la_naive_mla): the reference's naive
+// path (paths relative to the reference repo: src/naive_mla.cu:91-245 and the
+// PyTorch restatement tests/test_python.py:26-63) computed the way its math
+// reads, independently of the absorbed kernels:
+//   K_nope = c_t . W_UK^T   (S, nh*dn)      V = c_t . W_UV^T   (S, nh*dv)
+//   s[h,pos] = scale*(q_nope[h] . K_nope[pos,h] + q_rope[h] . RoPE(k_rope[pos], pos))
+//   out[h]   = softmax_pos(s[h]) . V[:,h]
+// all in fp32 from the 16-bit (or fp32) cache and weights. The reference's
+// cuBLAS call reads K/V transposed; this path does not reproduce that. It is
+// meant for checks at shapes where a CPU restatement is slow, so it favours
+// plainness over speed: a 64x64-tiled VALU GEMM for the decompression, one
+// thread per (head, position) for the scores, one workgroup per head for the
+// softmax and the weighted sum.
+#include "la_internal.hpp"
+
+namespace la {
+namespace {
+
+constexpr int kTile = 64;  // output tile of the decompression GEMM
+constexpr int kKStep = 16;
+
+// Y[r][n] = sum_c X[r][c] * W[n][c] for r < rows, n < N, c < K. X rows have
+// stride ldx elements (the cache row), W rows stride K. 256 threads, each
+// 4 x 4 outputs; X and W tiles staged through LDS transposed ([c][r]).
+template <typename XT, typename WT>
+__global__ __launch_bounds__(256) void decompress_kernel(const XT* __restrict__ X, int ldx, const WT* __restrict__ W,
+                                                         float* __restrict__ Y, int rows, int N, int K) {
+  __shared__ float xs[kKStep][kTile + 4];
+  __shared__ float ws[kKStep][kTile + 4];
+  const int r0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  float acc[4][4] = {};
+  for (int c0 = 0; c0 < K; c0 += kKStep) {
+    for (int i = threadIdx.x; i < kTile * kKStep; i += 256) {
+      const int rr = i / kKStep, cc = i % kKStep;
+      const int r = r0 + rr, n = n0 + rr, c = c0 + cc;
+      xs[cc][rr] = (r < rows && c < K) ? to_f32(X[(int64_t)r * ldx + c]) : 0.f;
+      ws[cc][rr] = (n < N && c < K) ? to_f32(W[(int64_t)n * K + c]) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int cc = 0; cc < kKStep; ++cc) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = xs[cc][ty + 16 * i];
+        b[i] = ws[cc][tx + 16 * i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * b[j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + ty + 16 * i;
+    if (r >= rows) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + tx + 16 * j;
+      if (n < N) Y[(int64_t)r * N + n] = acc[i][j];
+    }
+  }
+}
+
+// s[h][pos] for one query: thread per (pos, head), RoPE of the key by its
+// position (rotate-half, src/fused_mla.cu:43-51; positions past the table use
+// its last row).
+template <typename KT>
+__global__ __launch_bounds__(256) void naive_scores_kernel(const KT* __restrict__ kv, int S, int dc, int dR,
+                                                           const float* __restrict__ Kn, int nh, int dn,
+                                                           const float* __restrict__ q_nope,
+                                                           const float* __restrict__ q_rope,
+                                                           const float* __restrict__ cos_t,
+                                                           const float* __restrict__ sin_t, int64_t rope_rows,
+                                                           float scale, float* __restrict__ scores) {
+  const int pos = blockIdx.x * 256 + threadIdx.x;
+  const int h = blockIdx.y;
+  if (pos >= S) return;
+  const float* k = Kn + ((int64_t)pos * nh + h) * dn;
+  const float* q = q_nope + (int64_t)h * dn;
+  float a = 0.f;
+  for (int i = 0; i < dn; ++i) a += q[i] * k[i];
+  const int half = dR >> 1;
+  const int64_t r = (rope_rows > 0 && pos >= rope_rows) ? rope_rows - 1 : pos;
+  const KT* kr = kv + (int64_t)pos * (dc + dR) + dc;
+  const float* qr = q_rope + (int64_t)h * dR;
+  float b = 0.f;
+  for (int i = 0; i < half; ++i) {
+    const float k0 = to_f32(kr[i]), k1 = to_f32(kr[i + half]);
+    const float c = cos_t[r * half + i], s = sin_t[r * half + i];
+    b += qr[i] * (k0 * c - k1 * s) + qr[i + half] * (k0 * s + k1 * c);
+  }
+  scores[(int64_t)h * S + pos] = scale * a + scale * b;
+}
+
+// out[h][j] = sum_pos softmax(s[h])[pos] * V[pos][h*dv + j]: one workgroup per
+// head; max and sum reduced over the workgroup, then thread j < dv sums over
+// positions.
+__global__ __launch_bounds__(256) void naive_softmax_pv_kernel(const float* __restrict__ scores, int S,
+                                                               const float* __restrict__ V, int nh, int dv,
+                                                               float* __restrict__ out) {
+  const int h = blockIdx.x;
+  const float* s = scores + (int64_t)h * S;
+  __shared__ float red[8];
+  __shared__ float stat[2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (S == 0) {  // empty cache: zero output (as the absorbed path gives)
+    for (int j = tid; j < dv; j += 256) out[(int64_t)h * dv + j] = 0.f;
+    return;
+  }
+  float m = -INFINITY;
+  for (int p = tid; p < S; p += 256) m = fmaxf(m, s[p]);
+  m = wave_max(m);
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  if (tid == 0) stat[0] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  m = stat[0];
+  float l = 0.f;
+  for (int p = tid; p < S; p += 256) l += expf(s[p] - m);
+  l = wave_sum(l);
+  if (lane == 0) red[4 + wave] = l;
+  __syncthreads();
+  if (tid == 0) stat[1] = (red[4] + red[5]) + (red[6] + red[7]);
+  __syncthreads();
+  const float inv_l = 1.f / stat[1];
+  for (int j = tid; j < dv; j += 256) {
+    float acc = 0.f;
+    for (int p = 0; p < S; ++p) acc += expf(s[p] - m) * V[((int64_t)p * nh + h) * dv + j];
+    out[(int64_t)h * dv + j] = acc * inv_l;
+  }
+}
+
+template <typename XT, typename WT>
+hipError_t decompress(const NaiveProblem& p, const void* W, float* Y, int N, hipStream_t stream) {
+  const dim3 grid((unsigned)((N + kTile - 1) / kTile), (unsigned)((p.S + kTile - 1) / kTile));
+  hipLaunchKernelGGL((decompress_kernel<XT, WT>), grid, dim3(256), 0, stream, reinterpret_cast<const XT*>(p.kv),
+                     p.dc + p.dR, reinterpret_cast<const WT*>(W), Y, p.S, N, p.dc);
+  return hipGetLastError();
+}
+
+template <typename XT>
+hipError_t decompress_w(const NaiveProblem& p, const void* W, int wdt, float* Y, int N, hipStream_t stream) {
+  if (wdt == LA_DTYPE_BF16) return decompress<XT, __hip_bfloat16>(p, W, Y, N, stream);
+  if (wdt == LA_DTYPE_F16) return decompress<XT, __half>(p, W, Y, N, stream);
+  return decompress<XT, float>(p, W, Y, N, stream);
+}
+
+template <typename KT>
+hipError_t run_naive_t(const NaiveProblem& p, hipStream_t stream) {
+  if (p.S == 0) {
+    hipLaunchKernelGGL(naive_softmax_pv_kernel, dim3((unsigned)p.nh), dim3(256), 0, stream, p.scores, 0, p.V, p.nh,
+                       p.dv, p.out);
+    return hipGetLastError();
+  }
+  hipError_t e = decompress_w<KT>(p, p.W_UK, p.wuk_dtype, p.Kn, p.nh * p.dn, stream);
+  if (e == hipSuccess) e = decompress_w<KT>(p, p.W_UV, p.wuv_dtype, p.V, p.nh * p.dv, stream);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(naive_scores_kernel<KT>, dim3((unsigned)((p.S + 255) / 256), (unsigned)p.nh), dim3(256), 0,
+                     stream, reinterpret_cast<const KT*>(p.kv), p.S, p.dc, p.dR, p.Kn, p.nh, p.dn, p.q_nope,
+                     p.q_rope, p.rope_cos, p.rope_sin, p.rope_rows, p.scale, p.scores);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(naive_softmax_pv_kernel, dim3((unsigned)p.nh), dim3(256), 0, stream, p.scores, p.S, p.V, p.nh,
+                     p.dv, p.out);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t naive_workspace_bytes(int64_t S, int nh, int dn, int dv) {
+  const auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  return up((size_t)S * nh * dn * 4) + up((size_t)S * nh * dv * 4) + up((size_t)S * nh * 4);
+}
+
+hipError_t launch_naive(NaiveProblem p, void* workspace, hipStream_t stream) {
+  const auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  char* w = static_cast<char*>(workspace);
+  p.Kn = reinterpret_cast<float*>(w);
+  p.V = reinterpret_cast<float*>(w + up((size_t)p.S * p.nh * p.dn * 4));
+  p.scores = reinterpret_cast<float*>(w + up((size_t)p.S * p.nh * p.dn * 4) + up((size_t)p.S * p.nh * p.dv * 4));
+  if (p.kv_dtype == LA_DTYPE_BF16) return run_naive_t<__hip_bfloat16>(p, stream);
+  if (p.kv_dtype == LA_DTYPE_F16) return run_naive_t<__half>(p, stream);
+  return run_naive_t<float>(p, stream);
+}
+
+}  // namespace la

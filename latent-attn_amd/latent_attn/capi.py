@@ -113,6 +113,10 @@ def load() -> ctypes.CDLL:
     lib.la_fused_mla_workspace_size.argtypes = [i32, i32, cfgp]
     lib.la_absorb_q.restype = i32
     lib.la_absorb_q.argtypes = [vp, vp, i32, vp, i32, cfgp, vp]
+    lib.la_naive_mla.restype = i32
+    lib.la_naive_mla.argtypes = [vp, i32, i32, vp, i32, vp, i32, vp, vp, vp, vp, vp, cfgp, vp, sz, vp]
+    lib.la_naive_mla_workspace_size.restype = sz
+    lib.la_naive_mla_workspace_size.argtypes = [i32, cfgp]
     lib.la_append_kv.restype = i32
     lib.la_append_kv.argtypes = [ctypes.POINTER(AppendArgs), vp]
     _lib = lib

@@ -264,3 +264,22 @@ def test_cpp_dropin_header_compiles_and_links(tmp_path):
                     "-I" + os.path.join(REPO, "include"), str(src), "-o", str(exe), "-L" + libdir,
                     "-llatent_attn_hip", "-Wl,-rpath," + libdir], check=True)
     assert subprocess.run([str(exe)]).returncode == 0
+
+
+def test_naive_rejects_bad_arguments_and_sizes_its_workspace():
+    lib = capi.load()
+    cfg = capi.config(MLAConfig.deepseek_v2())
+    f = 0x1000
+    ok = [f, capi.LA_DTYPE_BF16, 16, f, capi.LA_DTYPE_BF16, f, capi.LA_DTYPE_BF16, f, f, f, f, f]
+    for i, bad in [(1, 9), (2, -1), (3, 0), (4, 7), (5, 0), (7, 0), (8, 0), (9, 0), (10, 0), (11, 0)]:
+        args = list(ok)
+        args[i] = bad
+        assert lib.la_naive_mla(*args, ctypes.byref(cfg), None, 0, None) == capi.LA_ERROR_INVALID_VALUE, i
+    # too small a caller workspace is refused before any launch
+    assert lib.la_naive_mla(*ok, ctypes.byref(cfg), 0x2000, 16, None) == capi.LA_ERROR_WORKSPACE
+    # fp32 K_nope (S, H*dn), V (S, H*dv) and scores (H, S), each 256-B aligned
+    S = 1000
+    up = lambda x: (x + 255) // 256 * 256
+    want = up(S * 128 * 128 * 4) + up(S * 128 * 128 * 4) + up(S * 128 * 4)
+    assert lib.la_naive_mla_workspace_size(S, ctypes.byref(cfg)) == want
+    assert lib.la_naive_mla_workspace_size(-1, ctypes.byref(cfg)) == 0
