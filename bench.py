@@ -197,6 +197,60 @@ def time_append(lib, hip, capi, inp, stream, calls: int = 100) -> float:
     return us
 
 
+def time_paged(lib, hip, capi, inp, out, ws, stream, bs: int = 64, steps: int = 100) -> dict:
+    """The same decode step over a paged copy of the cache: every sequence's
+    rows in blocks of `bs` rows scattered over a pool by a fixed permutation,
+    read through a block table with device lengths (la_decode_args.block_table).
+    Step time over `steps` steps and the attention kernel's time (10 x 10
+    back-to-back launches), as for the contiguous line."""
+    import numpy as np
+    import torch
+
+    B, S = inp["B"], inp["seq_len"]
+    dev = inp["kv"].device
+    bps = S // bs
+    perm = torch.from_numpy(np.random.RandomState(7).permutation(B * bps).astype(np.int32)).to(dev)
+    pool = torch.empty_like(inp["kv"])
+    pool.view(B * bps, bs, -1)[perm.long()] = inp["kv"].view(B * bps, bs, -1)
+    table = perm.view(B, bps).contiguous()
+    lens = torch.full((B,), S, dtype=torch.int32, device=dev)
+    a = decode_args(inp, out, capi)
+    a.kv_cache = pool.data_ptr()
+    a.seq_len = 0
+    a.seq_lens = lens.data_ptr()
+    a.block_table, a.block_size, a.blocks_per_seq = table.data_ptr(), bs, bps
+    need = lib.la_mla_decode_workspace_size(ctypes.byref(a))
+    assert 0 < need <= ws.numel()
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+
+    def step(ev_b=None, ev_e=None, repeat=0):
+        a.decode_event_begin, a.decode_event_end, a.decode_repeat = ev_b, ev_e, repeat
+        st = lib.la_mla_decode(ctypes.byref(a), ctypes.c_void_p(stream))
+        if st != 0:
+            raise RuntimeError(f"la_mla_decode (paged): {lib.la_status_string(st).decode()}")
+
+    for _ in range(50):
+        step()
+    t0, t1 = new_event(hip), new_event(hip)
+    torch.cuda.synchronize()
+    hip.hipEventRecord(t0, ctypes.c_void_p(stream))
+    for _ in range(steps):
+        step()
+    hip.hipEventRecord(t1, ctypes.c_void_p(stream))
+    hip.hipEventSynchronize(t1)
+    us_step = elapsed_ms(hip, t0, t1) * 1e3 / steps
+    evs = [(new_event(hip, True), new_event(hip, True)) for _ in range(10)]
+    for b, e in evs:
+        step(b, e, 10)
+    torch.cuda.synchronize()
+    kern = sorted(elapsed_ms(hip, b, e) / 10 for b, e in evs)
+    for ev in (t0, t1, *[x for pair in evs for x in pair]):
+        hip.hipEventDestroy(ev)
+    kern_us = sum(kern) / len(kern) * 1e3
+    return {"step_us": round(us_step, 2), "attn_kernel_us": round(kern_us, 2),
+            "frac_of_8TBps": round(int(inp["total"]) * BYTES_PER_POS / (kern_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
 def time_layer(hip, inp, stream, calls: int = 20) -> dict:
     """LatentAttentionLayer.forward_batch (DeepSeek-V2 dims, fp32 parameters
     as in the reference module) for one token per sequence over the
@@ -389,6 +443,7 @@ def main():
     ms_step = ms_total / K
     us_step = ms_step * 1e3
     append_us = time_append(lib, hip, capi, inp, stream)
+    paged = time_paged(lib, hip, capi, inp, out, ws, stream) if inp["offsets"] is None else None
     layer = time_layer(hip, inp, stream) if args.layer else None
 
     total_pos = int(inp["total"])
@@ -426,6 +481,7 @@ def main():
         "attn_kernel_us_min_max": [round(kern_ms[0] * 1e3, 2), round(kern_ms[-1] * 1e3, 2)],
         "mfma_frac_of_bf16_peak": round(flops_attn / (kern_avg * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         "append_kernel_us": round(append_us, 2),
+        **({"paged_block64": paged} if paged else {}),
         **({"layer_forward_batch": layer} if layer else {}),
         "roofline": {
             "bound": "hbm",

@@ -142,6 +142,17 @@ typedef struct la_decode_args {
    * NULL: each sequence is its whole region. The split plan covers the
    * regions, so capacity far beyond the lengths costs idle blocks. */
   const int32_t* seq_lens;
+  /* optional paged cache (block tables): kv_cache is then a pool of
+   * total_rows rows in blocks of block_size rows (total_rows a multiple of
+   * block_size), and position p of sequence s lives in pool row
+   * block_table[s*blocks_per_seq + p/block_size]*block_size + p%block_size
+   * (DEVICE int32 table, num_seqs*blocks_per_seq entries; ids outside the
+   * pool are clamped into it). seq_lens is required, seq_offsets must be
+   * NULL, seq_len is ignored. block_size a multiple of 32 keeps the MFMA
+   * kernel (others run on the VALU kernel). NULL: contiguous cache. */
+  const int32_t* block_table;
+  int32_t block_size;
+  int32_t blocks_per_seq;
 } la_decode_args;
 
 /* Arguments of la_append_kv. */
@@ -183,6 +194,14 @@ typedef struct la_append_args {
    * length change, no query rotation); never cleared by the library. */
   int32_t* status;
   la_mla_config cfg;
+  /* optional paged cache, as in la_decode_args: kv_cache is a pool of
+   * total_rows rows in blocks of block_size rows, sequence s has
+   * blocks_per_seq blocks listed in the DEVICE int32 block_table (capacity
+   * blocks_per_seq*block_size); seq_offsets must be NULL and seq_capacity is
+   * ignored. NULL: contiguous cache. */
+  const int32_t* block_table;
+  int32_t block_size;
+  int32_t blocks_per_seq;
 } la_append_args;
 
 /* Human-readable name of an la_status value. */

@@ -180,7 +180,8 @@ namespace {
 torch::Tensor run_decode(la_decode_args& a, const torch::Tensor& kv_cache, const torch::Tensor& q_rope,
                          const torch::Tensor& W_UV, const torch::Tensor& rope_cos, const torch::Tensor& rope_sin,
                          const c10::optional<torch::Tensor>& seq_offsets, const c10::optional<torch::Tensor>& seq_lens,
-                         const la_mla_config& cfg, int64_t batch, int chunk_rows, int kernel_variant) {
+                         const la_mla_config& cfg, int64_t batch, int chunk_rows, int kernel_variant,
+                         const c10::optional<torch::Tensor>& block_table, int block_size) {
   const int64_t row = cfg.kv_lora_rank + cfg.qk_rope_head_dim;
   TORCH_CHECK(q_rope.dim() == 3 && q_rope.size(0) == batch && q_rope.size(1) == cfg.num_heads &&
                   q_rope.size(2) == cfg.qk_rope_head_dim,
@@ -194,7 +195,21 @@ torch::Tensor run_decode(la_decode_args& a, const torch::Tensor& kv_cache, const
   a.num_seqs = (int32_t)batch;
   a.queries_per_seq = 1;
   int64_t longest = 0;
-  if (seq_offsets.has_value() && seq_offsets->defined()) {
+  if (block_table.has_value() && block_table->defined()) {
+    const auto& bt = *block_table;
+    TORCH_CHECK(bt.dtype() == torch::kInt32 && bt.is_contiguous() && bt.is_cuda() && bt.dim() == 2 &&
+                    bt.size(0) == batch,
+                "block_table must be a contiguous int32 CUDA tensor (batch, blocks_per_seq)");
+    TORCH_CHECK(!(seq_offsets.has_value() && seq_offsets->defined()), "block_table and seq_offsets exclude each other");
+    TORCH_CHECK(seq_lens.has_value() && seq_lens->defined(), "a paged cache needs seq_lens");
+    TORCH_CHECK(block_size > 0 && kv_cache.dim() == 2 && kv_cache.size(1) == row && kv_cache.size(0) % block_size == 0,
+                "paged kv_cache must be a (num_blocks * block_size, ", row, ") pool");
+    check_same_device(kv_cache, bt, "block_table");
+    a.total_rows = kv_cache.size(0);
+    a.block_table = bt.data_ptr<int32_t>();
+    a.block_size = block_size;
+    a.blocks_per_seq = (int32_t)bt.size(1);
+  } else if (seq_offsets.has_value() && seq_offsets->defined()) {
     const auto& off = *seq_offsets;
     TORCH_CHECK(off.dtype() == torch::kInt32 && off.is_contiguous() && off.is_cuda(),
                 "seq_offsets must be a contiguous int32 CUDA tensor");
@@ -253,7 +268,8 @@ torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, t
                                  torch::Tensor rope_sin, c10::optional<torch::Tensor> seq_offsets, int d_model,
                                  int kv_lora_rank, int qk_nope_head_dim, int qk_rope_head_dim, int num_heads,
                                  int v_head_dim, int chunk_rows, int kernel_variant,
-                                 c10::optional<torch::Tensor> seq_lens) {
+                                 c10::optional<torch::Tensor> seq_lens, c10::optional<torch::Tensor> block_table,
+                                 int block_size) {
   check_storage(kv_cache, "kv_cache");
   check_fp32_contiguous(q_nope, "q_nope");
   check_fp32_contiguous(q_rope, "q_rope");
@@ -274,7 +290,7 @@ torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, t
   a.W_UK = W_UK.data_ptr();
   a.w_uk_dtype = dtype_tag(W_UK);
   return run_decode(a, kv_cache, q_rope, W_UV, rope_cos, rope_sin, seq_offsets, seq_lens, cfg, q_nope.size(0),
-                    chunk_rows, kernel_variant);
+                    chunk_rows, kernel_variant, block_table, block_size);
 }
 
 // mla_decode_absorbed_forward -- the same step for queries already absorbed
@@ -284,7 +300,8 @@ torch::Tensor mla_decode_absorbed_forward(torch::Tensor kv_cache, torch::Tensor 
                                           torch::Tensor W_UV, torch::Tensor rope_cos, torch::Tensor rope_sin,
                                           c10::optional<torch::Tensor> seq_offsets, int d_model, int kv_lora_rank,
                                           int qk_nope_head_dim, int qk_rope_head_dim, int num_heads, int v_head_dim,
-                                          int chunk_rows, int kernel_variant, c10::optional<torch::Tensor> seq_lens) {
+                                          int chunk_rows, int kernel_variant, c10::optional<torch::Tensor> seq_lens,
+                                          c10::optional<torch::Tensor> block_table, int block_size) {
   check_storage(kv_cache, "kv_cache");
   check_fp32_contiguous(q_absorbed, "q_absorbed");
   check_fp32_contiguous(q_rope, "q_rope");
@@ -299,7 +316,7 @@ torch::Tensor mla_decode_absorbed_forward(torch::Tensor kv_cache, torch::Tensor 
   la_decode_args a{};
   a.q_absorbed = q_absorbed.data_ptr<float>();
   return run_decode(a, kv_cache, q_rope, W_UV, rope_cos, rope_sin, seq_offsets, seq_lens, cfg, q_absorbed.size(0),
-                    chunk_rows, kernel_variant);
+                    chunk_rows, kernel_variant, block_table, block_size);
 }
 
 // append_kv_forward -- device-side LatentKVCache::append_host
@@ -314,7 +331,8 @@ void append_kv_forward(torch::Tensor kv_cache, torch::Tensor seq_lens, torch::Te
                        c10::optional<torch::Tensor> q_rope, c10::optional<torch::Tensor> rope_cos,
                        c10::optional<torch::Tensor> rope_sin, c10::optional<torch::Tensor> seq_offsets,
                        c10::optional<torch::Tensor> status, int d_model, int kv_lora_rank, int qk_nope_head_dim,
-                       int qk_rope_head_dim, int num_heads, int v_head_dim) {
+                       int qk_rope_head_dim, int num_heads, int v_head_dim, c10::optional<torch::Tensor> block_table,
+                       int block_size) {
   check_storage(kv_cache, "kv_cache");
   check_storage(c_t, "c_t");
   check_storage(k_rope, "k_rope");
@@ -346,7 +364,20 @@ void append_kv_forward(torch::Tensor kv_cache, torch::Tensor seq_lens, torch::Te
   a.k_rope = k_rope.data_ptr();
   a.src_dtype = dtype_tag(c_t);
   a.cfg = cfg;
-  if (seq_offsets.has_value() && seq_offsets->defined()) {
+  if (block_table.has_value() && block_table->defined()) {
+    const auto& bt = *block_table;
+    TORCH_CHECK(bt.dtype() == torch::kInt32 && bt.is_contiguous() && bt.is_cuda() && bt.dim() == 2 &&
+                    bt.size(0) == batch,
+                "block_table must be a contiguous int32 CUDA tensor (batch, blocks_per_seq)");
+    TORCH_CHECK(!(seq_offsets.has_value() && seq_offsets->defined()), "block_table and seq_offsets exclude each other");
+    TORCH_CHECK(block_size > 0 && kv_cache.dim() == 2 && kv_cache.size(1) == row && kv_cache.size(0) % block_size == 0,
+                "paged kv_cache must be a (num_blocks * block_size, ", row, ") pool");
+    check_same_device(kv_cache, bt, "block_table");
+    a.total_rows = kv_cache.size(0);
+    a.block_table = bt.data_ptr<int32_t>();
+    a.block_size = block_size;
+    a.blocks_per_seq = (int32_t)bt.size(1);
+  } else if (seq_offsets.has_value() && seq_offsets->defined()) {
     const auto& off = *seq_offsets;
     TORCH_CHECK(off.dtype() == torch::kInt32 && off.is_contiguous() && off.is_cuda(),
                 "seq_offsets must be a contiguous int32 CUDA tensor");
@@ -474,18 +505,19 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("rope_cos"), py::arg("rope_sin"), py::arg("seq_offsets"), py::arg("d_model"),
         py::arg("kv_lora_rank"), py::arg("qk_nope_head_dim"), py::arg("qk_rope_head_dim"), py::arg("num_heads"),
         py::arg("v_head_dim"), py::arg("chunk_rows") = 0, py::arg("kernel_variant") = 0,
-        py::arg("seq_lens") = py::none());
+        py::arg("seq_lens") = py::none(), py::arg("block_table") = py::none(), py::arg("block_size") = 0);
   m.def("mla_decode_absorbed_forward", &mla_decode_absorbed_forward,
         "Batched MLA decode step for pre-absorbed queries (split-KV, combine, W_UV)", py::arg("kv_cache"),
         py::arg("q_absorbed"), py::arg("q_rope"), py::arg("W_UV"), py::arg("rope_cos"), py::arg("rope_sin"),
         py::arg("seq_offsets"), py::arg("d_model"), py::arg("kv_lora_rank"), py::arg("qk_nope_head_dim"),
         py::arg("qk_rope_head_dim"), py::arg("num_heads"), py::arg("v_head_dim"), py::arg("chunk_rows") = 0,
-        py::arg("kernel_variant") = 0, py::arg("seq_lens") = py::none());
+        py::arg("kernel_variant") = 0, py::arg("seq_lens") = py::none(), py::arg("block_table") = py::none(),
+        py::arg("block_size") = 0);
   m.def("append_kv_forward", &append_kv_forward,
         "Device-side append of latent rows at each sequence's length, with the query's RoPE",
         py::arg("kv_cache"), py::arg("seq_lens"), py::arg("c_t"), py::arg("k_rope"), py::arg("q_rope"),
         py::arg("rope_cos"), py::arg("rope_sin"), py::arg("seq_offsets"), py::arg("status"), py::arg("d_model"),
         py::arg("kv_lora_rank"), py::arg("qk_nope_head_dim"), py::arg("qk_rope_head_dim"), py::arg("num_heads"),
-        py::arg("v_head_dim"));
+        py::arg("v_head_dim"), py::arg("block_table") = py::none(), py::arg("block_size") = 0);
   m.def("absorb_q_forward", &absorb_q_forward, "q_absorbed = q_nope . W_UK per head");
 }

@@ -46,10 +46,13 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendProblem p)
   __shared__ int64_t first_row;  // row of the first new token, -1 = no room
   __shared__ int old_len;
   if (threadIdx.x == 0) {
-    const int64_t start = p.offsets ? (int64_t)p.offsets[s] : (int64_t)s * p.capacity;
-    const int64_t end = p.offsets ? (int64_t)p.offsets[s + 1] : start + p.capacity;
+    // paged: a virtual region of blocks_per_seq blocks (rows are mapped below)
+    const int64_t start = p.block_table ? 0 : p.offsets ? (int64_t)p.offsets[s] : (int64_t)s * p.capacity;
+    const int64_t end = p.block_table ? (int64_t)p.blocks_per_seq * p.block_size
+                        : p.offsets   ? (int64_t)p.offsets[s + 1]
+                                      : start + p.capacity;
     const int len = p.lens[s];
-    const bool ok = start >= 0 && start <= end && end <= p.total_rows && len >= 0 &&
+    const bool ok = start >= 0 && start <= end && (p.block_table || end <= p.total_rows) && len >= 0 &&
                     (int64_t)len + p.tokens <= end - start;
     first_row = ok ? start + len : -1;
     old_len = len;
@@ -68,7 +71,14 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendProblem p)
     const int c = i - t * row;
     const float v = c < p.dc ? load_any(p.c_t, p.src_dtype, (tok0 + t) * p.dc + c)
                              : load_any(p.k_rope, p.src_dtype, (tok0 + t) * p.dR + (c - p.dc));
-    store_any(p.kv, p.kv_dtype, (row0 + t) * row + c, v);
+    int64_t dst = row0 + t;
+    if (p.block_table) {  // position len + t of sequence s in the pool (block id clamped into it)
+      const int64_t pos = (int64_t)len + t;
+      int64_t b = p.block_table[(int64_t)s * p.blocks_per_seq + pos / p.block_size];
+      b = b < 0 ? 0 : (b >= p.pool_blocks ? p.pool_blocks - 1 : b);
+      dst = b * p.block_size + pos % p.block_size;
+    }
+    store_any(p.kv, p.kv_dtype, dst * row + c, v);
   }
 
   if (p.q_rope) {

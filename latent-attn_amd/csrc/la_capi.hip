@@ -72,8 +72,16 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
     return LA_ERROR_INVALID_VALUE;
   if (a->num_seqs < 0 || a->queries_per_seq < 1 || a->total_rows < 0) return LA_ERROR_INVALID_VALUE;
   if (!valid_dtype(a->kv_dtype) || !valid_dtype(a->w_uv_dtype)) return LA_ERROR_INVALID_VALUE;
-  if (!a->seq_offsets && (a->seq_len < 0 || (int64_t)a->num_seqs * a->seq_len > a->total_rows))
+  const bool paged = a->block_table != nullptr;
+  if (paged) {
+    // pool of total_rows rows in blocks; sequences are virtual regions of
+    // blocks_per_seq blocks whose filled length comes from seq_lens
+    if (a->block_size <= 0 || a->blocks_per_seq <= 0 || a->seq_offsets || !a->seq_lens ||
+        a->total_rows % a->block_size != 0 || (int64_t)a->blocks_per_seq * a->block_size > INT32_MAX)
+      return LA_ERROR_INVALID_VALUE;
+  } else if (!a->seq_offsets && (a->seq_len < 0 || (int64_t)a->num_seqs * a->seq_len > a->total_rows)) {
     return LA_ERROR_INVALID_VALUE;
+  }
   const bool absorb = a->q_nope != nullptr;
   if (absorb == (a->q_absorbed != nullptr)) return LA_ERROR_INVALID_VALUE;
   if (absorb && (!a->W_UK || !valid_dtype(a->w_uk_dtype))) return LA_ERROR_INVALID_VALUE;
@@ -88,6 +96,14 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   p->seq_len = a->seq_offsets ? 0 : a->seq_len;
   p->offsets = a->seq_offsets;
   p->lens = a->seq_lens;
+  if (paged) {
+    p->block_table = a->block_table;
+    p->block_size = a->block_size;
+    p->blocks_per_seq = a->blocks_per_seq;
+    p->pool_blocks = a->total_rows / a->block_size;
+    p->seq_len = a->blocks_per_seq * a->block_size;       // virtual region per sequence
+    p->total_rows = (int64_t)a->num_seqs * p->seq_len;    // the virtual row space the plan covers
+  }
   p->qps = a->queries_per_seq;
   p->nh = c.num_heads;
   p->Hq = a->queries_per_seq * c.num_heads;
@@ -121,7 +137,7 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
     pl.mfma = true;
   }
 
-  const int64_t total = a->seq_offsets ? a->total_rows : (int64_t)a->num_seqs * a->seq_len;
+  const int64_t total = paged ? p->total_rows : a->seq_offsets ? a->total_rows : (int64_t)a->num_seqs * a->seq_len;
   const int ncu = cu_count();
   int64_t L;
   if (chunk_rows > 0) {
@@ -136,6 +152,7 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   }
   if (L > (int64_t)1 << 30) L = (int64_t)1 << 30;
   if (pl.mfma && L > mfma_max_chunk_rows()) L = mfma_max_chunk_rows();
+  if (paged && pl.mfma) L = (L + 63) / 64 * 64;  // MFMA tiles start block-aligned
   const int64_t nchunks = total > 0 ? (total + L - 1) / L : 0;
   if (nchunks > (int64_t)1 << 30) return LA_ERROR_INVALID_VALUE;
   pl.chunk_len = (int)L;
@@ -410,8 +427,13 @@ int la_append_kv(const la_append_args* a, void* stream) {
   if (!a || !la::valid_cfg(&a->cfg) || !la::valid_dtype(a->kv_dtype) || !la::valid_dtype(a->src_dtype))
     return LA_ERROR_INVALID_VALUE;
   if (a->num_seqs < 0 || a->tokens_per_seq < 0 || a->total_rows < 0 || a->rope_rows < 0) return LA_ERROR_INVALID_VALUE;
-  if (!a->seq_offsets && (a->seq_capacity < 0 || (int64_t)a->num_seqs * a->seq_capacity > a->total_rows))
+  const bool paged = a->block_table != nullptr;
+  if (paged) {
+    if (a->block_size <= 0 || a->blocks_per_seq <= 0 || a->seq_offsets || a->total_rows % a->block_size != 0)
+      return LA_ERROR_INVALID_VALUE;
+  } else if (!a->seq_offsets && (a->seq_capacity < 0 || (int64_t)a->num_seqs * a->seq_capacity > a->total_rows)) {
     return LA_ERROR_INVALID_VALUE;
+  }
   if (a->num_seqs == 0) return LA_SUCCESS;
   if (!a->seq_lens || (a->total_rows > 0 && !a->kv_cache)) return LA_ERROR_INVALID_VALUE;
   if (a->tokens_per_seq > 0 && (!a->c_t || !a->k_rope)) return LA_ERROR_INVALID_VALUE;
@@ -448,6 +470,12 @@ int la_append_kv(const la_append_args* a, void* stream) {
   p.status = a->status;
   p.dc = a->cfg.kv_lora_rank;
   p.dR = a->cfg.qk_rope_head_dim;
+  if (paged) {
+    p.block_table = a->block_table;
+    p.block_size = a->block_size;
+    p.blocks_per_seq = a->blocks_per_seq;
+    p.pool_blocks = a->total_rows / a->block_size;
+  }
   const hipError_t e = la::launch_append(p, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? (int)LA_SUCCESS : la::record_hip(e);
 }

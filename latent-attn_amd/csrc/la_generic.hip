@@ -71,8 +71,8 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic_kernel(DecodeP
     for (int j = 0; j < NC; ++j) acc[j] = 0.f;
 
     for (int64_t r = lo + wave; r < seg_hi; r += kGenericWaves) {
-      const KT* row = kv + r * p.row_elems;
       const int64_t pos = r - s_lo;
+      const KT* row = kv + (p.block_table ? paged_row(p, s, pos) : r) * p.row_elems;
       float part = 0.f;
       float cv[NC];
 #pragma unroll

@@ -48,6 +48,14 @@ struct DecodeProblem {
   int seq_len;            // used when offsets == nullptr
   const int32_t* offsets; // device, num_seqs + 1, or nullptr
   const int32_t* lens;    // device, num_seqs, or nullptr: filled rows of each region
+  // paged cache (block_table != nullptr): kv is a pool of pool_blocks blocks
+  // of block_size rows; the row space above is virtual (sequence s owns
+  // [s * seq_len, (s+1) * seq_len), seq_len = blocks_per_seq * block_size),
+  // position pos of sequence s lives in pool row paged_row(p, s, pos)
+  const int32_t* block_table;  // device, num_seqs * blocks_per_seq
+  int block_size;
+  int blocks_per_seq;
+  int64_t pool_blocks;
   int qps;                // query tokens per sequence
   int nh;                 // weight heads
   int Hq;                 // query heads per sequence = qps * nh
@@ -104,6 +112,15 @@ __device__ inline int64_t seq_end(const DecodeProblem& p, int s) {
   const int64_t b = seq_begin(p, s);
   const int64_t l = p.lens[s];
   return l <= 0 ? b : (b + l < region_end ? b + l : region_end);
+}
+
+// Pool row of position pos of sequence s in a paged cache. Block ids are
+// clamped into the pool: a malformed table gives wrong rows, never an
+// out-of-bounds access. Requires pos < blocks_per_seq * block_size.
+__device__ inline int64_t paged_row(const DecodeProblem& p, int s, int64_t pos) {
+  int64_t b = p.block_table[(int64_t)s * p.blocks_per_seq + pos / p.block_size];
+  b = b < 0 ? 0 : (b >= p.pool_blocks ? p.pool_blocks - 1 : b);
+  return b * p.block_size + pos % p.block_size;
 }
 
 // RoPE table row of in-sequence position pos.
@@ -175,6 +192,12 @@ struct AppendProblem {
   int64_t rope_rows;
   int32_t* status;
   int dc, dR;
+  // paged cache (block_table != nullptr): as in DecodeProblem; capacity =
+  // blocks_per_seq * block_size, kv a pool of pool_blocks blocks
+  const int32_t* block_table;
+  int block_size;
+  int blocks_per_seq;
+  int64_t pool_blocks;
 };
 
 // One la_naive_mla call (la_naive.hip): a single query over one cache.

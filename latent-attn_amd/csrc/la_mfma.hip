@@ -417,28 +417,69 @@ constexpr int kRowBytes = (kDc + kDr) * 2;  // 1152: one packed cache row
 constexpr int kStreamPolicy = 2;
 
 struct SegCtx {
-  const char* base;  // first byte of the segment's first row
+  const char* base;  // contiguous cache: first byte of the segment's first row
   int64_t pos0;      // in-sequence position of the segment's first row
   int last;          // index of the segment's last row, relative to its first
+  int seq;           // sequence (paged cache: block-table row)
 };
 
-// Wave w's copies of tile k, rows tb = 32k + 8w ..: per-lane byte offset of
-// row tb's chunk lane (from the segment base), how far the segment's last row
-// is past tb (rows past it re-read the last row: their scores are masked),
-// and the k_rope copy's offset (row min(tb + lane/8, last), the logical
-// chunk (lane%8) ^ fr(row) that lands in chunk lane%8). Offsets stay below
-// 2^32 (segments are capped at kMaxChunkRows rows).
+// Tile k covers segment rows [32k, 32k + 32). The pipeline also copies up to
+// two tiles past the segment's last one; those copies re-read rows of the
+// last tile, so every copy of tile k reads rows of tile tile_eff(k) only.
+__device__ inline int tile_eff(const SegCtx& sg, int k) { return min(k, sg.last / kT); }
+
+// Paged cache: the block-table entry of tile k's rows. A tile never straddles
+// two blocks: block_size and the segment's first position are multiples of
+// 32 (the launcher rounds chunk_len and requires block_size % 32 == 0).
+__device__ inline int tile_block_entry(const DecodeProblem& p, const SegCtx& sg, int k) {
+  const int64_t pos = sg.pos0 + (int64_t)tile_eff(sg, k) * kT;
+  return p.block_table[(int64_t)sg.seq * p.blocks_per_seq + pos / p.block_size];
+}
+// Starts loading tile k's entry into v (inline asm: the compiler neither
+// waits for it nor copies v while it is in flight). The caller's next
+// vmcnt(0) completes it; tie(v) after that wait marks v as produced there.
+__device__ inline void tile_block_entry_async(const DecodeProblem& p, const SegCtx& sg, int k, int& v) {
+  const int64_t pos = sg.pos0 + (int64_t)tile_eff(sg, k) * kT;
+  const int32_t* a = p.block_table + (int64_t)sg.seq * p.blocks_per_seq + pos / p.block_size;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(a));
+}
+// First byte of tile k's first row: contiguous cache (entry unused) or the
+// pool block given by its table entry (clamped into the pool).
+template <bool kPaged>
+__device__ inline const char* tile_base(const DecodeProblem& p, const SegCtx& sg, int k, int entry) {
+  const int t0 = tile_eff(sg, k) * kT;
+  if constexpr (kPaged) {
+    int64_t b = __builtin_amdgcn_readfirstlane(entry);
+    b = b < 0 ? 0 : (b >= p.pool_blocks ? p.pool_blocks - 1 : b);
+    const int64_t row = b * p.block_size + (sg.pos0 + t0) % p.block_size;
+    return reinterpret_cast<const char*>(p.kv) + row * kRowBytes;
+  } else {
+    return sg.base + (int64_t)t0 * kRowBytes;
+  }
+}
+
+// Wave w's copies of tile k, rows tb = 32k + 8w ..: the tile's base address,
+// the per-lane byte offset of row tb's chunk lane from it, how far the
+// segment's last row is past tb (rows past it re-read the last row: their
+// scores are masked), and the k_rope copy's offset (row min(tb + lane/8,
+// last), the logical chunk (lane%8) ^ fr(row) that lands in chunk lane%8).
+// Offsets are relative to the tile base (rows of tile_eff(k) only; for the
+// copies past the segment tb - 32 tile_eff(k) is large, but every row they
+// read is clamped to the last one, and the 32-bit sum wraps back to it).
 struct TileDma {
+  const char* base;
   uint32_t ct, rope;
   int dlast;  // last - tb, wave-uniform
 };
-__device__ inline TileDma tile_dma(const SegCtx& sg, int k, int wave, int lane) {
+__device__ inline TileDma tile_dma(const SegCtx& sg, int k, const char* base, int wave, int lane) {
   const int tb = k * kT + 8 * wave;
+  const int t0 = tile_eff(sg, k) * kT;
   const int rr = lane >> 3;
   TileDma d;
-  d.ct = (uint32_t)tb * kRowBytes + 16 * lane;
+  d.base = base;
+  d.ct = (uint32_t)(tb - t0) * kRowBytes + 16 * lane;
   d.dlast = sg.last - tb;
-  d.rope = (uint32_t)min(tb + rr, sg.last) * kRowBytes + kDc * 2 + 16 * ((lane & 7) ^ fr(8 * wave + rr));
+  d.rope = (uint32_t)(min(tb + rr, sg.last) - t0) * kRowBytes + kDc * 2 + 16 * ((lane & 7) ^ fr(8 * wave + rr));
   return d;
 }
 
@@ -454,10 +495,10 @@ __device__ inline void issue_copy(const DecodeProblem& p, const SegCtx& sg, int 
   const int r_first = 8 * wave;
   if constexpr (J < 8) {
     const int j = min(J, d.dlast);
-    __builtin_amdgcn_global_load_lds(sg.base + (d.ct + (uint32_t)(j * kRowBytes)),
+    __builtin_amdgcn_global_load_lds(d.base + (d.ct + (uint32_t)(j * kRowBytes)),
                                      (lds_void*)(L + buf + ct_row_off(r_first + J)), 16, 0, kStreamPolicy);
   } else if constexpr (J == 8) {
-    __builtin_amdgcn_global_load_lds(sg.base + d.rope, (lds_void*)(L + buf + kRopeOff + r_first * 128), 16, 0,
+    __builtin_amdgcn_global_load_lds(d.base + d.rope, (lds_void*)(L + buf + kRopeOff + r_first * 128), 16, 0,
                                      kStreamPolicy);
   } else {
     const int row = r_first + (lane >> 3);
@@ -469,10 +510,10 @@ __device__ inline void issue_copy(const DecodeProblem& p, const SegCtx& sg, int 
   }
 }
 
-// All kDmaPerWave copies of tile k.
-__device__ inline void issue_tile_dma(const DecodeProblem& p, const SegCtx& sg, int k, lchar* L, uint32_t buf,
-                                      int wave, int lane) {
-  const TileDma d = tile_dma(sg, k, wave, lane);
+// All kDmaPerWave copies of tile k (base: tile_base of tile k).
+__device__ inline void issue_tile_dma(const DecodeProblem& p, const SegCtx& sg, int k, const char* base, lchar* L,
+                                      uint32_t buf, int wave, int lane) {
+  const TileDma d = tile_dma(sg, k, base, wave, lane);
   static_for<kDmaPerWave>([&](auto j) { issue_copy<decltype(j)::value>(p, sg, k, L, buf, wave, lane, d); });
 }
 
@@ -551,7 +592,7 @@ __device__ inline void block_coords(int num_chunks, int groups, int* chunk, int*
   *chunk = x * per + k / groups;
 }
 
-template <typename KT>
+template <typename KT, bool kPaged>
 __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, int groups) {
   typedef Ops<KT> O_;
   typedef typename O_::vec vec;
@@ -584,18 +625,30 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     }
     const int64_t seg_hi = min(hi, s_hi);
     SegCtx sg;
-    sg.base = reinterpret_cast<const char*>(p.kv) + lo * kRowBytes;
+    sg.base = reinterpret_cast<const char*>(p.kv) + (kPaged ? 0 : lo * kRowBytes);
     sg.pos0 = lo - s_lo;
     sg.last = (int)(seg_hi - lo - 1);
+    sg.seq = s;
     const int seg_len = sg.last + 1;
     const int ntiles = (seg_len + kT - 1) / kT;
 
     lds_barrier();  // all waves are done with the previous segment's buffers
 
+    // paged cache: the table entries of tiles 0 and 1 (tile 1 is copied in
+    // iteration -1); iteration t loads the entry of tile t+3 into blk_cur once
+    // its own copies have their base, for the next iteration
+    int blk_cur = 0;
+    const char* base0 = tile_base<kPaged>(p, sg, 0, 0);
+    if constexpr (kPaged) {
+      const int e0 = tile_block_entry(p, sg, 0);
+      blk_cur = tile_block_entry(p, sg, 1);
+      base0 = tile_base<kPaged>(p, sg, 0, e0);
+    }
+
     // tile 1 rides along iteration -1; a fresh lane index keeps the per-lane
     // addresses out of the registers (and spill slots) that live across the
     // prologue: a spill reload here would wait on vmcnt and so serialise the copies
-    issue_tile_dma(p, sg, 0, L, 0, wave, lane_id());
+    issue_tile_dma(p, sg, 0, base0, L, 0, wave, lane_id());
 
     // Q^T as the B operand: lane holds Q[head][16kk + 8*g2 .. +8], pre-scaled.
     // q_prep is stored in operand order (qprep_index): the wave's 32 rows form
@@ -671,6 +724,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     }
     for (int t = -1; t < ntiles; ++t) {
       wait_vm<0>();   // this wave's copies of tile t+1 (issued in iteration t-1) have landed
+      if constexpr (kPaged) tie(blk_cur);  // and the table entry loaded with them
       lds_barrier();  // tile t+1 staged and rotated by every wave; iteration t-1 done
       const int lane = lane_id();
       const int g2 = lane >> 5;
@@ -713,7 +767,11 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       const uint32_t ct_x = nxt + ct_row_off(arow) + 16 * g2;
       const uint32_t rp_x = (nxt + kRopeOff + arow * 128) | (16 * (g2 ^ fr(arow)));
       const uint32_t pp_x = kPtabOff + par * kPtabPar + pw * 2048 + 16 * lane;
-      const TileDma dm = tile_dma(sg, t + 2, wave, lane);
+      // paged: this iteration's copies use tile t+2's entry (loaded in the
+      // previous iteration or the prologue); tile t+3's goes out now and is
+      // waited for by the next iteration's vmcnt(0)
+      const TileDma dm = tile_dma(sg, t + 2, tile_base<kPaged>(p, sg, t + 2, blk_cur), wave, lane);
+      if constexpr (kPaged) tile_block_entry_async(p, sg, t + 3, blk_cur);
       auto a_rd = [&](auto kk_c) -> vec {
         constexpr int kk = decltype(kk_c)::value;
         if constexpr (kk < 32) return lds_rd128<vec, 32 * kk>(L, ct_x);
@@ -1066,11 +1124,11 @@ __global__ __launch_bounds__(256) void prep_q_kernel(const float* __restrict__ q
   *reinterpret_cast<vec*>(out + qprep_index(qrow, 8 * j)) = v;
 }
 
-template <typename KT>
+template <typename KT, bool kPaged>
 hipError_t launch_t(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
   static bool attr_set = false;  // per instance; setting it twice is harmless
   if (!attr_set) {
-    const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<KT>);
+    const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<KT, kPaged>);
     hipFuncAttributes fa;
     hipError_t e = hipFuncGetAttributes(&fa, fn);
     if (e != hipSuccess) return e;
@@ -1083,11 +1141,11 @@ hipError_t launch_t(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_be
   const int64_t blocks = (int64_t)((p.num_chunks + 7) / 8) * 8 * groups;
   if (ev_begin || ev_end) {
     // the events time this kernel's execution alone (no dispatch gap)
-    hipExtLaunchKernelGGL((decode_mfma_kernel<KT>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, stream,
-                          ev_begin, ev_end, 0, p, groups);
+    hipExtLaunchKernelGGL((decode_mfma_kernel<KT, kPaged>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes,
+                          stream, ev_begin, ev_end, 0, p, groups);
   } else {
-    hipLaunchKernelGGL((decode_mfma_kernel<KT>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, stream, p,
-                       groups);
+    hipLaunchKernelGGL((decode_mfma_kernel<KT, kPaged>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, stream,
+                       p, groups);
   }
   return hipGetLastError();
 }
@@ -1116,6 +1174,8 @@ bool mfma_supported(const DecodeProblem& p) {
   if (p.kv_dtype != LA_DTYPE_BF16 && p.kv_dtype != LA_DTYPE_F16) return false;
   if (p.dc != kDc || p.dR != kDr || p.Hq % 16 != 0 || p.Hq <= 0) return false;
   if (p.rope_rows > (1 << 24) || (p.rope_rows == 0 && p.total_rows > (1 << 24))) return false;
+  // paged: a 32-row tile must lie inside one block
+  if (p.block_table && (p.block_size % kT != 0 || p.chunk_len % kT != 0)) return false;
   // 16-byte aligned cache rows, table rows and query rows
   if ((reinterpret_cast<uintptr_t>(p.kv) & 15) || (reinterpret_cast<uintptr_t>(p.rope_cos) & 15) ||
       (reinterpret_cast<uintptr_t>(p.rope_sin) & 15) || (reinterpret_cast<uintptr_t>(p.q_rope) & 15) ||
@@ -1139,8 +1199,12 @@ hipError_t launch_prep_q(const DecodeProblem& p, hipStream_t stream) {
 }
 
 hipError_t launch_decode_mfma(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
-  if (p.kv_dtype == LA_DTYPE_BF16) return launch_t<__hip_bfloat16>(p, stream, ev_begin, ev_end);
-  return launch_t<__half>(p, stream, ev_begin, ev_end);
+  if (p.block_table) {
+    if (p.kv_dtype == LA_DTYPE_BF16) return launch_t<__hip_bfloat16, true>(p, stream, ev_begin, ev_end);
+    return launch_t<__half, true>(p, stream, ev_begin, ev_end);
+  }
+  if (p.kv_dtype == LA_DTYPE_BF16) return launch_t<__hip_bfloat16, false>(p, stream, ev_begin, ev_end);
+  return launch_t<__half, false>(p, stream, ev_begin, ev_end);
 }
 
 }  // namespace la

@@ -56,6 +56,9 @@ class DecodeArgs(ctypes.Structure):
         ("decode_event_end", ctypes.c_void_p),
         ("decode_repeat", ctypes.c_int32),
         ("seq_lens", ctypes.c_void_p),
+        ("block_table", ctypes.c_void_p),
+        ("block_size", ctypes.c_int32),
+        ("blocks_per_seq", ctypes.c_int32),
     ]
 
 
@@ -79,6 +82,9 @@ class AppendArgs(ctypes.Structure):
         ("rope_rows", ctypes.c_int64),
         ("status", ctypes.c_void_p),
         ("cfg", MlaConfig),
+        ("block_table", ctypes.c_void_p),
+        ("block_size", ctypes.c_int32),
+        ("blocks_per_seq", ctypes.c_int32),
     ]
 
 

@@ -119,6 +119,8 @@ def mla_decode(
     chunk_rows: int = 0,
     kernel_variant: int = 0,
     seq_lens: Optional[torch.Tensor] = None,
+    block_table: Optional[torch.Tensor] = None,
+    block_size: int = 0,
 ) -> torch.Tensor:
     """One decode step for a batch of sequences, each with its own cache.
 
@@ -137,13 +139,18 @@ def mla_decode(
         seq_lens:    optional int32 (batch,) device tensor; sequence b is the
                      first seq_lens[b] rows of its region (a capacity cache
                      filled by ``append_kv``)
+        block_table, block_size: optional paged cache: kv_cache is a pool of
+                     (num_blocks * block_size, dc + dR) rows and position p of
+                     sequence b lives in row block_table[b, p // block_size] *
+                     block_size + p % block_size (int32 (batch, blocks_per_seq)
+                     device tensor; needs seq_lens)
 
     Returns:
         (batch, num_heads, v_head_dim) fp32
     """
     _C = _load_ext()
     return _C.mla_decode_forward(kv_cache, q_nope, q_rope, W_UK, W_UV, rope_cos, rope_sin, seq_offsets,
-                                 *_cfg_args(cfg), chunk_rows, kernel_variant, seq_lens)
+                                 *_cfg_args(cfg), chunk_rows, kernel_variant, seq_lens, block_table, block_size)
 
 
 def mla_decode_absorbed(
@@ -158,13 +165,16 @@ def mla_decode_absorbed(
     seq_lens: Optional[torch.Tensor] = None,
     chunk_rows: int = 0,
     kernel_variant: int = 0,
+    block_table: Optional[torch.Tensor] = None,
+    block_size: int = 0,
 ) -> torch.Tensor:
     """``mla_decode`` for queries already in latent space: q_absorbed
     (batch, num_heads, kv_lora_rank) fp32 (e.g. x . W_Q_absorbed^T). Same
     cache / sequence arguments; returns (batch, num_heads, v_head_dim) fp32."""
     _C = _load_ext()
     return _C.mla_decode_absorbed_forward(kv_cache, q_absorbed, q_rope, W_UV, rope_cos, rope_sin, seq_offsets,
-                                          *_cfg_args(cfg), chunk_rows, kernel_variant, seq_lens)
+                                          *_cfg_args(cfg), chunk_rows, kernel_variant, seq_lens, block_table,
+                                          block_size)
 
 
 def append_kv(
@@ -178,6 +188,8 @@ def append_kv(
     rope_sin: Optional[torch.Tensor] = None,
     seq_offsets: Optional[torch.Tensor] = None,
     status: Optional[torch.Tensor] = None,
+    block_table: Optional[torch.Tensor] = None,
+    block_size: int = 0,
 ) -> None:
     """Append new latent rows to every sequence's cache on the device.
 
@@ -199,10 +211,12 @@ def append_kv(
                      queries_per_seq appended tokens (needs rope_cos/sin)
         status:      optional int32 device tensor; element 0 is set to 1 when
                      a sequence has no room (that sequence is left unchanged)
+        block_table, block_size: optional paged cache, as in ``mla_decode``
+                     (capacity block_table.shape[1] * block_size per sequence)
     """
     _C = _load_ext()
     _C.append_kv_forward(kv_cache, seq_lens, c_t, k_rope, q_rope, rope_cos, rope_sin, seq_offsets, status,
-                         *_cfg_args(cfg))
+                         *_cfg_args(cfg), block_table, block_size)
 
 
 def absorb_q(q_nope: torch.Tensor, W_UK: torch.Tensor, cfg: "MLAConfig") -> torch.Tensor:

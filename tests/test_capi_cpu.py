@@ -283,3 +283,25 @@ def test_naive_rejects_bad_arguments_and_sizes_its_workspace():
     want = up(S * 128 * 128 * 4) + up(S * 128 * 128 * 4) + up(S * 128 * 4)
     assert lib.la_naive_mla_workspace_size(S, ctypes.byref(cfg)) == want
     assert lib.la_naive_mla_workspace_size(-1, ctypes.byref(cfg)) == 0
+
+
+@pytest.mark.parametrize("field,value", [
+    ("block_size", 0),
+    ("blocks_per_seq", 0),
+    ("seq_lens", 0),            # a paged cache needs device lengths
+    ("seq_offsets", 0x3000),    # block tables and packed offsets exclude each other
+    ("total_rows", 100),        # the pool is whole blocks
+])
+def test_decode_rejects_bad_paged_arguments(field, value):
+    lib = capi.load()
+    a = _args(block_table=0x2000, block_size=64, blocks_per_seq=2, seq_lens=0x2100, total_rows=128, seq_len=0)
+    setattr(a, field, value)
+    assert lib.la_mla_decode(ctypes.byref(a), None) == capi.LA_ERROR_INVALID_VALUE
+
+
+def test_append_rejects_bad_paged_arguments():
+    lib = capi.load()
+    for field, value in (("block_size", 0), ("blocks_per_seq", -1), ("seq_offsets", 0x3000), ("total_rows", 100)):
+        a = _append_args(block_table=0x2000, block_size=64, blocks_per_seq=2, total_rows=256)
+        setattr(a, field, value)
+        assert lib.la_append_kv(ctypes.byref(a), None) == capi.LA_ERROR_INVALID_VALUE, field
