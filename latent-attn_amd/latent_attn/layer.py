@@ -93,16 +93,19 @@ class LatentAttentionLayer(nn.Module):
 
     @torch.no_grad()
     def forward_batch(self, x: torch.Tensor, kv_cache: torch.Tensor, seq_offsets: Optional[torch.Tensor] = None,
-                      seq_lens: Optional[torch.Tensor] = None) -> torch.Tensor:
+                      seq_lens: Optional[torch.Tensor] = None, block_table: Optional[torch.Tensor] = None,
+                      block_size: int = 0) -> torch.Tensor:
         """One decode token per sequence of a batch: x (batch, d_model);
         kv_cache (batch, seq_len, dc + dR), or packed (rows, dc + dR) with
         int32 seq_offsets (batch + 1,), optionally with device seq_lens
-        (capacity caches filled by ``functional.append_kv``). Row b of the
-        result equals ``forward(x[b], cache of sequence b)``. Returns
+        (capacity caches filled by ``functional.append_kv``), or a paged pool
+        with block_table / block_size (see ``functional.mla_decode``). Row b
+        of the result equals ``forward(x[b], cache of sequence b)``. Returns
         (batch, d_model) fp32."""
         if x.dim() != 2 or x.size(1) != self.cfg.d_model:
             raise ValueError(f"x must be (batch, {self.cfg.d_model})")
         q_abs, q_r = self._queries(x)
         out = F.mla_decode_absorbed(kv_cache, q_abs, q_r, self._w_uv_fp16(), self.rope_cos, self.rope_sin, self.cfg,
-                                    seq_offsets=seq_offsets, seq_lens=seq_lens)
+                                    seq_offsets=seq_offsets, seq_lens=seq_lens, block_table=block_table,
+                                    block_size=block_size)
         return out.reshape(x.size(0), -1) @ self.W_O.T

@@ -56,14 +56,17 @@ def gather(pool, table, bs):
 
 # chunk_rows: multiples of 64 for the MFMA kernel (the launcher rounds a paged
 # plan's chunks up to one, which would split the contiguous run differently)
-@pytest.mark.parametrize("bs,variant,chunk_rows", [(32, 0, 0), (64, 0, 0), (64, 2, 128), (256, 0, 192), (16, 0, 0),
-                                                   (64, 1, 0), (32, 1, 100)])
-def test_paged_decode_equals_contiguous(cuda, bs, variant, chunk_rows):
+@pytest.mark.parametrize("bs,variant,chunk_rows,dtype", [(32, 0, 0, torch.bfloat16), (64, 0, 0, torch.bfloat16),
+                                                         (64, 2, 128, torch.bfloat16), (256, 0, 192, torch.bfloat16),
+                                                         (16, 0, 0, torch.bfloat16), (64, 1, 0, torch.bfloat16),
+                                                         (32, 1, 100, torch.bfloat16), (64, 0, 0, torch.float16),
+                                                         (48, 0, 0, torch.float16)])
+def test_paged_decode_equals_contiguous(cuda, bs, variant, chunk_rows, dtype):
     cfg = MLAConfig.deepseek_v2()
-    B, cap = 4, 1024
-    lens0 = [1024, 1, 700, 0]
+    B, cap = 4, (1024 // bs) * bs  # whole blocks (1008 rows for 48-row blocks)
+    lens0 = [cap, 1, 700, 0]
     g = torch.Generator().manual_seed(51)
-    cache = torch.randn(B, cap, ROW, generator=g).to(torch.bfloat16).to(cuda)
+    cache = torch.randn(B, cap, ROW, generator=g).to(dtype).to(cuda)
     pool, table = scatter(cache, bs, 52)
     lens = torch.tensor(lens0, dtype=torch.int32, device=cuda)
     W_UK, W_UV = make_weights(cfg, "bf16", 53, cuda)
@@ -77,7 +80,7 @@ def test_paged_decode_equals_contiguous(cuda, bs, variant, chunk_rows):
                          kernel_variant=variant, block_table=table, block_size=bs)
     torch.cuda.synchronize()
     assert torch.equal(out_p, out_c), float((out_p - out_c).abs().max())
-    if bs == 64 and variant == 0:
+    if bs == 64 and variant == 0 and dtype == torch.bfloat16:
         d = mo.Dims(5120, 512, 128, 64, 128, 128)
         qa = mo.absorb_q(to_np(q_nope), to_np(W_UK), d)
         kv = to_np(cache)
