@@ -251,6 +251,40 @@ def time_paged(lib, hip, capi, inp, out, ws, stream, bs: int = 64, steps: int = 
             "frac_of_8TBps": round(int(inp["total"]) * BYTES_PER_POS / (kern_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
+def time_fp8(lib, hip, capi, inp, out, stream, steps: int = 20) -> dict:
+    """The same decode step over an FP8 E4M3 copy of the cache (half the
+    bytes; attention on the VALU kernel): microseconds per step over `steps`
+    steps, and the latent-cache rate against 8 TB/s at 576 B per position."""
+    import torch
+
+    kv8 = inp["kv"].to(torch.float8_e4m3fn)
+    a = decode_args(inp, out, capi)
+    a.kv_cache, a.kv_dtype = kv8.data_ptr(), capi.LA_DTYPE_FP8_E4M3
+    need = lib.la_mla_decode_workspace_size(ctypes.byref(a))
+    ws8 = torch.empty(need, dtype=torch.uint8, device=kv8.device)
+    a.workspace, a.workspace_bytes = ws8.data_ptr(), need
+
+    def step():
+        st = lib.la_mla_decode(ctypes.byref(a), ctypes.c_void_p(stream))
+        if st != 0:
+            raise RuntimeError(f"la_mla_decode (fp8): {lib.la_status_string(st).decode()}")
+
+    for _ in range(3):
+        step()
+    t0, t1 = new_event(hip), new_event(hip)
+    torch.cuda.synchronize()
+    hip.hipEventRecord(t0, ctypes.c_void_p(stream))
+    for _ in range(steps):
+        step()
+    hip.hipEventRecord(t1, ctypes.c_void_p(stream))
+    hip.hipEventSynchronize(t1)
+    us = elapsed_ms(hip, t0, t1) * 1e3 / steps
+    hip.hipEventDestroy(t0)
+    hip.hipEventDestroy(t1)
+    return {"step_us": round(us, 1),
+            "cache_frac_of_8TBps": round(int(inp["total"]) * BYTES_PER_POS / 2 / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
 def time_layer(hip, inp, stream, calls: int = 20) -> dict:
     """LatentAttentionLayer.forward_batch (DeepSeek-V2 dims, fp32 parameters
     as in the reference module) for one token per sequence over the
@@ -354,6 +388,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--fp8", action="store_true",
+                    help="also time the step over an FP8 E4M3 copy of the cache (VALU attention kernel)")
     ap.add_argument("--layer", action="store_true",
                     help="also time LatentAttentionLayer.forward_batch (fp32 projections, 1.8 GB of weights) "
                          "on the same batch and cache")
@@ -445,6 +481,7 @@ def main():
     append_us = time_append(lib, hip, capi, inp, stream)
     paged = time_paged(lib, hip, capi, inp, out, ws, stream) if inp["offsets"] is None else None
     layer = time_layer(hip, inp, stream) if args.layer else None
+    fp8 = time_fp8(lib, hip, capi, inp, out, stream) if args.fp8 else None
 
     total_pos = int(inp["total"])
     cache_bytes = total_pos * BYTES_PER_POS
@@ -483,6 +520,7 @@ def main():
         "append_kernel_us": round(append_us, 2),
         **({"paged_block64": paged} if paged else {}),
         **({"layer_forward_batch": layer} if layer else {}),
+        **({"fp8_cache": fp8} if fp8 else {}),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved_gbps, 1),

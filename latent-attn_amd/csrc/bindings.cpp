@@ -35,6 +35,7 @@ int dtype_tag(const torch::Tensor& t) {
     case torch::kFloat32: return LA_DTYPE_F32;
     case torch::kFloat16: return LA_DTYPE_F16;
     case torch::kBFloat16: return LA_DTYPE_BF16;
+    case torch::kFloat8_e4m3fn: return LA_DTYPE_FP8_E4M3;
     default: return -1;
   }
 }

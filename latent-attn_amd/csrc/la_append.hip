@@ -24,6 +24,7 @@ constexpr int kAppendThreads = 1024;
 __device__ inline void store_any(void* base, int dtype, int64_t i, float v) {
   if (dtype == LA_DTYPE_BF16) reinterpret_cast<__hip_bfloat16*>(base)[i] = __float2bfloat16(v);
   else if (dtype == LA_DTYPE_F16) reinterpret_cast<__half*>(base)[i] = __float2half(v);
+  else if (dtype == LA_DTYPE_FP8_E4M3) reinterpret_cast<uint8_t*>(base)[i] = f32_to_fp8(v);
   else reinterpret_cast<float*>(base)[i] = v;
 }
 

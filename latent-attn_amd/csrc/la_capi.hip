@@ -20,6 +20,8 @@ int record_hip(hipError_t e) {
 }
 
 bool valid_dtype(int d) { return d == LA_DTYPE_F32 || d == LA_DTYPE_F16 || d == LA_DTYPE_BF16; }
+// latent caches may also be FP8 E4M3 (weights may not)
+bool valid_cache_dtype(int d) { return valid_dtype(d) || d == LA_DTYPE_FP8_E4M3; }
 
 // Same conditions as MLAConfig::validate (src/mla_config.cuh:35-40) plus the
 // rotate-half requirement of an even rope dimension.
@@ -71,7 +73,7 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   if (chunk_rows < 0 || variant < kAuto || variant > kMfma || a->rope_rows < 0 || a->decode_repeat < 0)
     return LA_ERROR_INVALID_VALUE;
   if (a->num_seqs < 0 || a->queries_per_seq < 1 || a->total_rows < 0) return LA_ERROR_INVALID_VALUE;
-  if (!valid_dtype(a->kv_dtype) || !valid_dtype(a->w_uv_dtype)) return LA_ERROR_INVALID_VALUE;
+  if (!valid_cache_dtype(a->kv_dtype) || !valid_dtype(a->w_uv_dtype)) return LA_ERROR_INVALID_VALUE;
   const bool paged = a->block_table != nullptr;
   if (paged) {
     // pool of total_rows rows in blocks; sequences are virtual regions of
@@ -379,7 +381,7 @@ int la_naive_mla(const void* kv_cache, int kv_dtype, int seq_len, const void* W_
                  int w_uv_dtype, const float* q_nope, const float* q_rope, const float* rope_cos,
                  const float* rope_sin, float* output, const la_mla_config* cfg, void* workspace,
                  size_t workspace_bytes, void* stream) {
-  if (!la::valid_cfg(cfg) || seq_len < 0 || !la::valid_dtype(kv_dtype) || !la::valid_dtype(w_uk_dtype) ||
+  if (!la::valid_cfg(cfg) || seq_len < 0 || !la::valid_cache_dtype(kv_dtype) || !la::valid_dtype(w_uk_dtype) ||
       !la::valid_dtype(w_uv_dtype))
     return LA_ERROR_INVALID_VALUE;
   if (!W_UK || !W_UV || !q_nope || !q_rope || !rope_cos || !rope_sin || !output || (seq_len > 0 && !kv_cache))
@@ -424,7 +426,7 @@ int la_naive_mla(const void* kv_cache, int kv_dtype, int seq_len, const void* W_
 }
 
 int la_append_kv(const la_append_args* a, void* stream) {
-  if (!a || !la::valid_cfg(&a->cfg) || !la::valid_dtype(a->kv_dtype) || !la::valid_dtype(a->src_dtype))
+  if (!a || !la::valid_cfg(&a->cfg) || !la::valid_cache_dtype(a->kv_dtype) || !la::valid_cache_dtype(a->src_dtype))
     return LA_ERROR_INVALID_VALUE;
   if (a->num_seqs < 0 || a->tokens_per_seq < 0 || a->total_rows < 0 || a->rope_rows < 0) return LA_ERROR_INVALID_VALUE;
   const bool paged = a->block_table != nullptr;

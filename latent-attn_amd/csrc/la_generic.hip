@@ -259,7 +259,8 @@ __global__ __launch_bounds__(256) void absorb_kernel(const float* __restrict__ q
 
 bool generic_supported(const DecodeProblem& p) {
   return p.dc >= 1 && p.dc <= 1024 && p.dR >= 2 && p.dR <= 256 && (p.dR % 2) == 0 &&
-         (p.kv_dtype == LA_DTYPE_F32 || p.kv_dtype == LA_DTYPE_F16 || p.kv_dtype == LA_DTYPE_BF16);
+         (p.kv_dtype == LA_DTYPE_F32 || p.kv_dtype == LA_DTYPE_F16 || p.kv_dtype == LA_DTYPE_BF16 ||
+          p.kv_dtype == LA_DTYPE_FP8_E4M3);
 }
 
 hipError_t launch_decode_generic(const DecodeProblem& p, hipStream_t stream) {
@@ -267,6 +268,7 @@ hipError_t launch_decode_generic(const DecodeProblem& p, hipStream_t stream) {
     case LA_DTYPE_F32: return launch_generic_t<float>(p, stream);
     case LA_DTYPE_F16: return launch_generic_t<__half>(p, stream);
     case LA_DTYPE_BF16: return launch_generic_t<__hip_bfloat16>(p, stream);
+    case LA_DTYPE_FP8_E4M3: return launch_generic_t<fp8e4m3>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }

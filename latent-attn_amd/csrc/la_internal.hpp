@@ -142,6 +142,41 @@ __device__ inline int find_seq(const DecodeProblem& p, int64_t r) {
   return lo;
 }
 
+// OCP FP8 E4M3 (e4m3fn) latent-cache element: sign, 4 exponent bits (bias
+// 7), 3 mantissa bits; exponent 0 is subnormal (m * 2^-9), 0x7F / 0xFF NaN.
+struct fp8e4m3 {
+  uint8_t bits;
+};
+__device__ inline float fp8_to_f32(uint32_t c) {
+  const uint32_t e = (c >> 3) & 15, m = c & 7;
+  float v;
+  if (e == 15 && m == 7) v = __builtin_nanf("");
+  else if (e == 0) v = (float)m * 0x1p-9f;
+  else v = __builtin_amdgcn_ldexpf(1.f + (float)m * 0.125f, (int)e - 7);
+  return (c & 0x80) ? -v : v;
+}
+// Round to nearest even, saturating at +-448 (the largest finite value);
+// NaN stays NaN.
+__device__ inline uint8_t f32_to_fp8(float x) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, x);
+  const uint32_t s = (b >> 24) & 0x80;
+  const float a = __builtin_fabsf(x);
+  if (a != a) return (uint8_t)(s | 0x7F);
+  if (a >= 448.f) return (uint8_t)(s | 0x7E);
+  if (a < 0x1p-6f) return (uint8_t)(s | (uint32_t)__builtin_rintf(a * 512.f));  // subnormal; 8 = 2^-6
+  const uint32_t ab = __builtin_bit_cast(uint32_t, a);
+  uint32_t e = ((ab >> 23) & 0xFF) - 127 + 7;  // 1 .. 15
+  uint32_t m = (ab >> 20) & 7;
+  const uint32_t rem = ab & 0xFFFFF;
+  if (rem > 0x80000 || (rem == 0x80000 && (m & 1))) ++m;
+  if (m == 8) {
+    m = 0;
+    ++e;
+  }
+  const uint32_t c = (e << 3) | m;
+  return (uint8_t)(s | (c > 0x7E ? 0x7E : c));
+}
+
 template <typename T>
 __device__ inline float to_f32(T v);
 template <>
@@ -150,12 +185,15 @@ template <>
 __device__ inline float to_f32<__half>(__half v) { return __half2float(v); }
 template <>
 __device__ inline float to_f32<__hip_bfloat16>(__hip_bfloat16 v) { return __bfloat162float(v); }
+template <>
+__device__ inline float to_f32<fp8e4m3>(fp8e4m3 v) { return fp8_to_f32(v.bits); }
 
 // Load element i of a weight matrix whose dtype is only known at run time
 // (uniform across the launch, so the switch does not diverge).
 __device__ inline float load_any(const void* base, int dtype, int64_t i) {
   if (dtype == LA_DTYPE_BF16) return __bfloat162float(reinterpret_cast<const __hip_bfloat16*>(base)[i]);
   if (dtype == LA_DTYPE_F16) return __half2float(reinterpret_cast<const __half*>(base)[i]);
+  if (dtype == LA_DTYPE_FP8_E4M3) return fp8_to_f32(reinterpret_cast<const uint8_t*>(base)[i]);
   return reinterpret_cast<const float*>(base)[i];
 }
 

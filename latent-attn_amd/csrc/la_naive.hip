@@ -184,6 +184,7 @@ hipError_t launch_naive(NaiveProblem p, void* workspace, hipStream_t stream) {
   p.scores = reinterpret_cast<float*>(w + up((size_t)p.S * p.nh * p.dn * 4) + up((size_t)p.S * p.nh * p.dv * 4));
   if (p.kv_dtype == LA_DTYPE_BF16) return run_naive_t<__hip_bfloat16>(p, stream);
   if (p.kv_dtype == LA_DTYPE_F16) return run_naive_t<__half>(p, stream);
+  if (p.kv_dtype == LA_DTYPE_FP8_E4M3) return run_naive_t<fp8e4m3>(p, stream);
   return run_naive_t<float>(p, stream);
 }
 

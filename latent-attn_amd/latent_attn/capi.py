@@ -13,7 +13,7 @@ import os
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "liblatent_attn_hip.so")
 
 LA_SUCCESS, LA_ERROR_INVALID_VALUE, LA_ERROR_NOT_SUPPORTED, LA_ERROR_WORKSPACE, LA_ERROR_HIP = range(5)
-LA_DTYPE_F32, LA_DTYPE_F16, LA_DTYPE_BF16 = range(3)
+LA_DTYPE_F32, LA_DTYPE_F16, LA_DTYPE_BF16, LA_DTYPE_FP8_E4M3 = range(4)
 
 
 class MlaConfig(ctypes.Structure):

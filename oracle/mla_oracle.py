@@ -35,6 +35,9 @@ float32). Each function cites the reference code it restates:
   (``LatentAttentionLayer.forward``): q_abs = W_Q_absorbed x, q_rope =
   W_Q_rope x (not rotated), the absorbed attention with W_UV rounded to fp16
   (``_w_uv_fp16``, :98-99), then W_O over the flattened heads.
+* ``fp8_e4m3_encode`` / ``fp8_e4m3_decode`` -- the OCP FP8 E4M3 cache format
+  of this build (no reference counterpart): round to nearest even, saturating
+  at +-448.
 * ``rotate_queries``     -- rotate-half RoPE of q_rope (the pairing of
   /root/reference/src/fused_mla.cu:43-51 and tests/test_python.py:50-54) at
   the position of the token each query belongs to; the reference itself never
@@ -101,11 +104,47 @@ def f16_round(x: np.ndarray) -> np.ndarray:
     return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
 
 
+def fp8_e4m3_encode(x: np.ndarray) -> np.ndarray:
+    """float -> OCP FP8 E4M3 (e4m3fn) codes (uint8): round to nearest even,
+    saturate at +-448, NaN -> 0x7F | sign. The cache-write rule of this build
+    (la_append_kv); the reference has no fp8 cache. In range it equals
+    torch's float8_e4m3fn conversion (pinned in tests/test_oracle.py)."""
+    x = np.asarray(x, dtype=np.float32)
+    sign = (np.signbit(x)).astype(np.uint8) << 7
+    a = np.abs(x).astype(np.float64)
+    code = np.zeros(x.shape, dtype=np.int64)
+    nan = np.isnan(a)
+    sat = a >= 448.0
+    sub = a < 2.0 ** -6
+    code = np.where(sub, np.rint(a * 512.0), code)          # 0..8 (8 is 2^-6, the first normal)
+    norm = ~(nan | sat | sub)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        e = np.floor(np.log2(np.where(norm, a, 1.0)))
+        m = np.rint((np.where(norm, a, 1.0) / 2.0 ** e - 1.0) * 8.0)   # np.rint: half to even
+    e = np.where(m == 8, e + 1, e)
+    m = np.where(m == 8, 0, m)
+    code = np.where(norm, np.minimum(((e + 7) * 8 + m), 0x7E), code)
+    code = np.where(sat, 0x7E, code)
+    code = np.where(nan, 0x7F, code)
+    return (code.astype(np.uint8) | sign).astype(np.uint8)
+
+
+def fp8_e4m3_decode(c: np.ndarray) -> np.ndarray:
+    """OCP FP8 E4M3 codes -> float32 values."""
+    c = np.asarray(c, dtype=np.uint8).astype(np.int64)
+    e, m = (c >> 3) & 15, c & 7
+    v = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * 2.0 ** (e - 7))
+    v = np.where((e == 15) & (m == 7), np.nan, v)
+    return np.where(c & 0x80, -v, v).astype(np.float32)
+
+
 def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
     if dtype == "bf16":
         return bf16_round(x)
     if dtype == "f16":
         return f16_round(x)
+    if dtype == "fp8":
+        return fp8_e4m3_decode(fp8_e4m3_encode(x))
     return np.asarray(x, dtype=np.float32)
 
 

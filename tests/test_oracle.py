@@ -415,3 +415,43 @@ def test_layer_forward_is_linear_in_w_o_and_uses_unrotated_queries():
     qr = (p["W_Q_rope"] @ x).reshape(4, 8)
     out = mo.absorbed_mla(kv, qa, qr, mo.f16_round(p["W_UV"]), cos, sin, cfg)
     assert np.allclose(y1, p["W_O"] @ out.reshape(-1), rtol=1e-12, atol=1e-15)
+
+
+# ---- FP8 E4M3 cache format ----------------------------------------------
+
+def test_fp8_decode_known_codes_and_torch():
+    """Every one of the 256 codes decodes as torch's float8_e4m3fn does (a
+    library routine); spot values from the format's definition."""
+    import torch
+
+    codes = np.arange(256, dtype=np.uint8)
+    ours = mo.fp8_e4m3_decode(codes)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(np.isnan(ours), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(ours[ok], ref[ok])
+    assert mo.fp8_e4m3_decode(np.array([0x38, 0x7E, 0x01, 0x08, 0xB8], np.uint8)).tolist() == \
+        [1.0, 448.0, 2.0 ** -9, 2.0 ** -6, -1.0]
+
+
+def test_fp8_encode_rounds_to_nearest_even_and_saturates():
+    """In range the encoder equals torch's float8_e4m3fn conversion (round to
+    nearest even) on a dense sweep including every midpoint between codes;
+    beyond +-448 it saturates (torch gives NaN there); decode(encode(v)) == v
+    for every finite code value."""
+    import torch
+
+    codes = np.arange(256, dtype=np.uint8)
+    vals = mo.fp8_e4m3_decode(codes)
+    fin = vals[np.isfinite(vals)]
+    pos = np.unique(np.abs(fin))
+    mids = (pos[:-1] + pos[1:]) / 2
+    rs = np.random.RandomState(0)
+    sweep = np.concatenate([fin, mids, -mids, rs.uniform(-448, 448, 4000), rs.standard_normal(4000) * 1e-3]).astype(np.float32)
+    ours = mo.fp8_e4m3_encode(sweep)
+    ref = torch.from_numpy(sweep).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(ours, ref)
+    assert np.array_equal(mo.fp8_e4m3_encode(fin), codes[np.isfinite(vals)])
+    big = np.array([448.0, 460.0, 464.0, 500.0, 1e30, -1e30], np.float32)
+    assert mo.fp8_e4m3_encode(big).tolist() == [0x7E, 0x7E, 0x7E, 0x7E, 0x7E, 0xFE]
+    assert mo.fp8_e4m3_encode(np.array([np.nan], np.float32))[0] & 0x7F == 0x7F
