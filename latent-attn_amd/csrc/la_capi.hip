@@ -79,7 +79,8 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
     // pool of total_rows rows in blocks; sequences are virtual regions of
     // blocks_per_seq blocks whose filled length comes from seq_lens
     if (a->block_size <= 0 || a->blocks_per_seq <= 0 || a->seq_offsets || !a->seq_lens ||
-        a->total_rows % a->block_size != 0 || (int64_t)a->blocks_per_seq * a->block_size > INT32_MAX)
+        a->total_rows % a->block_size != 0 || (int64_t)a->blocks_per_seq * a->block_size > INT32_MAX ||
+        a->total_rows > (int64_t)UINT32_MAX)  // pool rows are 32-bit in the MFMA kernel
       return LA_ERROR_INVALID_VALUE;
   } else if (!a->seq_offsets && (a->seq_len < 0 || (int64_t)a->num_seqs * a->seq_len > a->total_rows)) {
     return LA_ERROR_INVALID_VALUE;
@@ -103,6 +104,8 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
     p->block_size = a->block_size;
     p->blocks_per_seq = a->blocks_per_seq;
     p->pool_blocks = a->total_rows / a->block_size;
+    p->pool_last = (int)std::min<int64_t>(std::max<int64_t>(p->pool_blocks - 1, 0), INT32_MAX);
+    set_tile_divisor(*p, (uint32_t)std::max(a->block_size / 32, 1));
     p->seq_len = a->blocks_per_seq * a->block_size;       // virtual region per sequence
     p->total_rows = (int64_t)a->num_seqs * p->seq_len;    // the virtual row space the plan covers
   }

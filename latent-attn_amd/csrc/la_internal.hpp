@@ -56,6 +56,13 @@ struct DecodeProblem {
   int block_size;
   int blocks_per_seq;
   int64_t pool_blocks;
+  // paged MFMA kernel (block_size % 32 == 0): 32-row tiles per block and the
+  // multiplier that divides by it, q / tile_per_block = (mulhi(q, tpb_magic)
+  // + q) >> tpb_shift for q < 2^31 (set by set_tile_divisor); pool_last =
+  // pool_blocks - 1, capped at INT32_MAX (table entries are int32)
+  uint32_t tile_per_block, tpb_magic;
+  int tpb_shift;
+  int pool_last;
   int qps;                // query tokens per sequence
   int nh;                 // weight heads
   int Hq;                 // query heads per sequence = qps * nh
@@ -116,6 +123,19 @@ __device__ inline int64_t seq_end(const DecodeProblem& p, int s) {
 
 // Pool row of position pos of sequence s in a paged cache. Block ids are
 // clamped into the pool: a malformed table gives wrong rows, never an
+// Division by an invariant d >= 1 with a multiply (Granlund & Montgomery,
+// "Division by invariant integers using multiplication", PLDI 1994, the
+// round-up multiplier): l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1,
+// then q / d = (floor(q m / 2^32) + q) >> l for every q < 2^31 (the sum fits
+// in 32 bits there).
+inline void set_tile_divisor(DecodeProblem& p, uint32_t d) {
+  int l = 0;
+  while ((1ull << l) < d) ++l;
+  p.tile_per_block = d;
+  p.tpb_shift = l;
+  p.tpb_magic = (uint32_t)((((1ull << l) - d) << 32) / d + 1);
+}
+
 // out-of-bounds access. Requires pos < blocks_per_seq * block_size.
 __device__ inline int64_t paged_row(const DecodeProblem& p, int s, int64_t pos) {
   int64_t b = p.block_table[(int64_t)s * p.blocks_per_seq + pos / p.block_size];

@@ -420,7 +420,9 @@ struct SegCtx {
   const char* base;  // contiguous cache: first byte of the segment's first row
   int64_t pos0;      // in-sequence position of the segment's first row
   int last;          // index of the segment's last row, relative to its first
-  int seq;           // sequence (paged cache: block-table row)
+  int seq;           // sequence
+  const int32_t* tab;  // paged cache: the sequence's block-table row
+  uint32_t tile0;      // paged cache: in-sequence tile index of the segment's first tile
 };
 
 // Tile k covers segment rows [32k, 32k + 32). The pipeline also copies up to
@@ -428,33 +430,38 @@ struct SegCtx {
 // last tile, so every copy of tile k reads rows of tile tile_eff(k) only.
 __device__ inline int tile_eff(const SegCtx& sg, int k) { return min(k, sg.last / kT); }
 
-// Paged cache: the block-table entry of tile k's rows. A tile never straddles
-// two blocks: block_size and the segment's first position are multiples of
-// 32 (the launcher rounds chunk_len and requires block_size % 32 == 0).
+// Paged cache: tile k is in-sequence tile q = tile0 + tile_eff(k), in block
+// q / tile_per_block at tile q % tile_per_block. A tile never straddles two
+// blocks: block_size and the segment's first position are multiples of 32
+// (the launcher rounds chunk_len and requires block_size % 32 == 0). q <
+// 2^26, so the launcher's multiplier divides exactly, in 32 bits.
+__device__ inline uint32_t tile_seq_index(const SegCtx& sg, int k) { return sg.tile0 + (uint32_t)tile_eff(sg, k); }
+__device__ inline uint32_t tile_block_index(const DecodeProblem& p, uint32_t q) {
+  return (__umulhi(q, p.tpb_magic) + q) >> p.tpb_shift;
+}
 __device__ inline int tile_block_entry(const DecodeProblem& p, const SegCtx& sg, int k) {
-  const int64_t pos = sg.pos0 + (int64_t)tile_eff(sg, k) * kT;
-  return p.block_table[(int64_t)sg.seq * p.blocks_per_seq + pos / p.block_size];
+  return sg.tab[tile_block_index(p, tile_seq_index(sg, k))];
 }
 // Starts loading tile k's entry into v (inline asm: the compiler neither
 // waits for it nor copies v while it is in flight). The caller's next
 // vmcnt(0) completes it; tie(v) after that wait marks v as produced there.
 __device__ inline void tile_block_entry_async(const DecodeProblem& p, const SegCtx& sg, int k, int& v) {
-  const int64_t pos = sg.pos0 + (int64_t)tile_eff(sg, k) * kT;
-  const int32_t* a = p.block_table + (int64_t)sg.seq * p.blocks_per_seq + pos / p.block_size;
+  const int32_t* a = sg.tab + tile_block_index(p, tile_seq_index(sg, k));
   asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(a));
 }
 // First byte of tile k's first row: contiguous cache (entry unused) or the
-// pool block given by its table entry (clamped into the pool).
+// pool block given by its table entry (clamped into the pool; pool rows fit
+// in 32 bits, which the launcher checks).
 template <bool kPaged>
 __device__ inline const char* tile_base(const DecodeProblem& p, const SegCtx& sg, int k, int entry) {
-  const int t0 = tile_eff(sg, k) * kT;
   if constexpr (kPaged) {
-    int64_t b = __builtin_amdgcn_readfirstlane(entry);
-    b = b < 0 ? 0 : (b >= p.pool_blocks ? p.pool_blocks - 1 : b);
-    const int64_t row = b * p.block_size + (sg.pos0 + t0) % p.block_size;
-    return reinterpret_cast<const char*>(p.kv) + row * kRowBytes;
+    const uint32_t q = tile_seq_index(sg, k);
+    const uint32_t in_block = q - tile_block_index(p, q) * p.tile_per_block;
+    const int b = min(max(__builtin_amdgcn_readfirstlane(entry), 0), p.pool_last);
+    const uint32_t row = (uint32_t)b * (uint32_t)p.block_size + in_block * kT;
+    return reinterpret_cast<const char*>(p.kv) + (uint64_t)row * kRowBytes;
   } else {
-    return sg.base + (int64_t)t0 * kRowBytes;
+    return sg.base + (int64_t)(tile_eff(sg, k) * kT) * kRowBytes;
   }
 }
 
@@ -629,6 +636,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     sg.pos0 = lo - s_lo;
     sg.last = (int)(seg_hi - lo - 1);
     sg.seq = s;
+    sg.tab = kPaged ? p.block_table + (int64_t)s * p.blocks_per_seq : nullptr;
+    sg.tile0 = (uint32_t)(sg.pos0 / kT);
     const int seg_len = sg.last + 1;
     const int ntiles = (seg_len + kT - 1) / kT;
 

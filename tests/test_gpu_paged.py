@@ -56,11 +56,13 @@ def gather(pool, table, bs):
 
 # chunk_rows: multiples of 64 for the MFMA kernel (the launcher rounds a paged
 # plan's chunks up to one, which would split the contiguous run differently)
+# 96- and 160-row blocks hold 3 and 5 tiles: the MFMA kernel's divide by tiles per block
 @pytest.mark.parametrize("bs,variant,chunk_rows,dtype", [(32, 0, 0, torch.bfloat16), (64, 0, 0, torch.bfloat16),
                                                          (64, 2, 128, torch.bfloat16), (256, 0, 192, torch.bfloat16),
                                                          (16, 0, 0, torch.bfloat16), (64, 1, 0, torch.bfloat16),
                                                          (32, 1, 100, torch.bfloat16), (64, 0, 0, torch.float16),
-                                                         (48, 0, 0, torch.float16)])
+                                                         (48, 0, 0, torch.float16), (96, 0, 128, torch.bfloat16),
+                                                         (160, 2, 128, torch.float16)])
 def test_paged_decode_equals_contiguous(cuda, bs, variant, chunk_rows, dtype):
     cfg = MLAConfig.deepseek_v2()
     B, cap = 4, (1024 // bs) * bs  # whole blocks (1008 rows for 48-row blocks)
