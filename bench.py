@@ -253,7 +253,7 @@ def time_paged(lib, hip, capi, inp, out, ws, stream, bs: int = 64, steps: int = 
 
 def time_fp8(lib, hip, capi, inp, out, stream, steps: int = 20) -> dict:
     """The same decode step over an FP8 E4M3 copy of the cache (half the
-    bytes; attention on the VALU kernel): microseconds per step over `steps`
+    bytes; staged as bf16 for the MFMA kernel): microseconds per step over `steps`
     steps, and the latent-cache rate against 8 TB/s at 576 B per position."""
     import torch
 
@@ -389,7 +389,7 @@ def main():
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fp8", action="store_true",
-                    help="also time the step over an FP8 E4M3 copy of the cache (VALU attention kernel)")
+                    help="also time the step over an FP8 E4M3 copy of the cache (bf16 staging + MFMA attention kernel)")
     ap.add_argument("--layer", action="store_true",
                     help="also time LatentAttentionLayer.forward_batch (fp32 projections, 1.8 GB of weights) "
                          "on the same batch and cache")

@@ -61,6 +61,9 @@ struct Plan {
   size_t part_scale_off = 0;
   bool absorb_mfma = false;  // q_nope . W_UK on the MFMA kernel
   bool absorb_prep = false;  // ... writing the attention kernel's 16-bit Q rows directly
+  bool stage_fp8 = false;    // fp8 cache staged as bf16 for the MFMA kernel
+  size_t stage_off = 0;
+  int64_t stage_elems = 0;
   size_t q_abs_off = 0, q_prep_off = 0, part_o_off = 0, part_lse_off = 0, o_merged_off = 0, total = 0;
 };
 
@@ -133,6 +136,18 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   if (a->total_rows > 0 && !a->kv_cache) return LA_ERROR_INVALID_VALUE;
 
   Plan pl;
+  // An FP8 E4M3 cache goes to the MFMA kernel through a bf16 copy in the
+  // workspace (every E4M3 value is a bf16 value), row for row, so offsets,
+  // lengths and block tables address it unchanged. The VALU kernel
+  // (kernel_variant 1) reads the fp8 rows directly.
+  bool stage = false;
+  if (p->kv_dtype == LA_DTYPE_FP8_E4M3 && variant != kGeneric &&
+      (reinterpret_cast<uintptr_t>(a->kv_cache) & 15) == 0 && a->total_rows * p->row_elems % 16 == 0) {
+    DecodeProblem ps = *p;
+    ps.kv_dtype = LA_DTYPE_BF16;
+    stage = mfma_supported(ps);
+    if (stage) p->kv_dtype = LA_DTYPE_BF16;
+  }
   const bool mfma_ok = mfma_supported(*p);
   if (variant == kMfma && !mfma_ok) return LA_ERROR_NOT_SUPPORTED;
   if (variant == kGeneric || !mfma_ok) {
@@ -193,6 +208,12 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
     pl.o_merged_off = off;
     off += align_up(combine_project_mfma_workspace(*p));
   }
+  if (stage) {
+    pl.stage_fp8 = true;
+    pl.stage_off = off;
+    pl.stage_elems = a->total_rows * (int64_t)p->row_elems;
+    off += align_up((size_t)pl.stage_elems * 2);
+  }
   pl.total = off;
 
   p->chunk_len = pl.chunk_len;
@@ -232,6 +253,13 @@ int run(const la_decode_args* a, hipStream_t stream) {
 
   const la_mla_config& c = a->cfg;
   const int64_t tokens = (int64_t)a->num_seqs * a->queries_per_seq;
+  if (plan.stage_fp8) {
+    p.kv = ws + plan.stage_off;
+    if (plan.num_chunks > 0) {
+      hipError_t e = launch_fp8_to_bf16(a->kv_cache, ws + plan.stage_off, plan.stage_elems, stream);
+      if (e != hipSuccess) return finish(e);
+    }
+  }
   if (plan.mfma) p.q_prep = ws + plan.q_prep_off;
   if (a->q_nope) {
     hipError_t e = hipSuccess;
@@ -358,12 +386,12 @@ size_t la_fused_mla_workspace_size(int seq_len, int batch_size, const la_mla_con
   if (!cfg || seq_len < 0 || batch_size <= 0) return 0;
   // Only plan-relevant fields are read. The kernel family is not known here
   // (it depends on dtype and pointer alignment), so return the larger of the
-  // two plans.
+  // plans (an fp8 cache's includes its bf16 staging copy).
   alignas(256) static const char dummy[256] = {0};
   const float* d = reinterpret_cast<const float*>(dummy);
   size_t best = 0;
   for (int variant : {1, 2}) {
-    for (int dt : {LA_DTYPE_F16, LA_DTYPE_F32}) {
+    for (int dt : {LA_DTYPE_F16, LA_DTYPE_F32, LA_DTYPE_FP8_E4M3}) {
       la_decode_args a = la::shared_cache_args(dummy, dt, seq_len, batch_size, d, d, dummy, dt, d, d,
                                                const_cast<float*>(d), cfg, nullptr, 0);
       a.kernel_variant = variant;

@@ -121,8 +121,6 @@ __device__ inline int64_t seq_end(const DecodeProblem& p, int s) {
   return l <= 0 ? b : (b + l < region_end ? b + l : region_end);
 }
 
-// Pool row of position pos of sequence s in a paged cache. Block ids are
-// clamped into the pool: a malformed table gives wrong rows, never an
 // Division by an invariant d >= 1 with a multiply (Granlund & Montgomery,
 // "Division by invariant integers using multiplication", PLDI 1994, the
 // round-up multiplier): l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1,
@@ -136,6 +134,8 @@ inline void set_tile_divisor(DecodeProblem& p, uint32_t d) {
   p.tpb_magic = (uint32_t)((((1ull << l) - d) << 32) / d + 1);
 }
 
+// Pool row of position pos of sequence s in a paged cache. Block ids are
+// clamped into the pool: a malformed table gives wrong rows, never an
 // out-of-bounds access. Requires pos < blocks_per_seq * block_size.
 __device__ inline int64_t paged_row(const DecodeProblem& p, int s, int64_t pos) {
   int64_t b = p.block_table[(int64_t)s * p.blocks_per_seq + pos / p.block_size];
@@ -288,6 +288,8 @@ hipError_t launch_naive(NaiveProblem p, void* workspace, hipStream_t stream);
 
 // Device-side cache append + query RoPE.
 hipError_t launch_append(const AppendProblem& p, hipStream_t stream);
+// elems FP8 E4M3 values at src -> bf16 at dst (exact); elems % 16 == 0, both 16-byte aligned
+hipError_t launch_fp8_to_bf16(const void* src, void* dst, int64_t elems, hipStream_t stream);
 
 // VALU split-KV decode: any dtype, kv_lora_rank <= 1024, qk_rope_head_dim <= 256.
 hipError_t launch_decode_generic(const DecodeProblem& p, hipStream_t stream);

@@ -1,9 +1,12 @@
 """GPU parity of FP8 E4M3 latent caches (LA_DTYPE_FP8_E4M3, torch.float8_e4m3fn).
 
 The cache values are exactly the fp8 codes' values (oracle fp8_e4m3_decode);
-every kernel computes in fp32 from them, so decode and the naive path are
-held to the fp32 tolerance against the float64 oracle (tests/conftest.py:
-assert_close). Appends are byte work: the stored codes must equal the
+the VALU decode kernel (kernel_variant 1) and the naive path compute in fp32
+from them and are held to the fp32 tolerance against the float64 oracle
+(tests/conftest.py:assert_close). The default decode stages the fp8 rows as
+bf16 (exactly: every E4M3 value is a bf16 value) for the MFMA kernel, so it
+is held to the bf16 tolerance, and must equal that kernel run on a bf16 copy
+of the cache bit for bit, contiguous and paged. Appends are byte work: the stored codes must equal the
 oracle's encoding (round to nearest even, saturating at +-448) exactly.
 """
 
@@ -35,8 +38,9 @@ def fp8_np(t):
     return mo.fp8_e4m3_decode(t.view(torch.uint8).cpu().numpy()).astype(np.float64)
 
 
+@pytest.mark.parametrize("variant,tol", [(1, "f32"), (0, "bf16")])
 @pytest.mark.parametrize("lens0", [[500, 1, 333], [64, 0, 7]])
-def test_fp8_decode_matches_oracle(cuda, lens0):
+def test_fp8_decode_matches_oracle(cuda, lens0, variant, tol):
     cfg = MLAConfig.deepseek_v2()
     B, cap = 3, 500
     kv = fp8_cache((B, cap, ROW), 81, cuda)
@@ -44,14 +48,41 @@ def test_fp8_decode_matches_oracle(cuda, lens0):
     W_UK, W_UV = make_weights(cfg, "bf16", 82, cuda)
     q_nope, q_rope = make_queries((B,), cfg, 83, cuda)
     cos, sin = rope(cap, cfg, cuda)
-    out = F.mla_decode(kv, q_nope, q_rope, W_UK, W_UV, cos, sin, cfg, seq_lens=lens)
+    out = F.mla_decode(kv, q_nope, q_rope, W_UK, W_UV, cos, sin, cfg, seq_lens=lens, kernel_variant=variant)
     torch.cuda.synchronize()
     kv_np = fp8_np(kv)
     packed = np.concatenate([kv_np[b, :lens0[b]] for b in range(B)])
     offsets = np.concatenate([[0], np.cumsum(lens0)])
     qa = mo.absorb_q(to_np(q_nope), to_np(W_UK), D)
     ref = mo.decode_sequences(packed, offsets, qa, to_np(q_rope), to_np(W_UV), to_np(cos), to_np(sin), D)
-    assert_close(out.cpu().numpy(), ref, "f32", f"fp8 decode {lens0}")
+    assert_close(out.cpu().numpy(), ref, tol, f"fp8 decode {lens0} variant {variant}")
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_fp8_staged_decode_equals_bf16_mfma(cuda, paged):
+    """The default fp8 decode (bf16 staging + MFMA kernel) gives exactly what
+    the MFMA kernel gives on a bf16 copy of the cache: the staging is exact
+    and the rest of the path is the same."""
+    cfg = MLAConfig.deepseek_v2()
+    B, cap, bs = 3, 512, 64
+    kv = fp8_cache((B, cap, ROW), 111, cuda)
+    lens = torch.tensor([512, 77, 300], dtype=torch.int32, device=cuda)
+    W_UK, W_UV = make_weights(cfg, "bf16", 112, cuda)
+    q_nope, q_rope = make_queries((B,), cfg, 113, cuda)
+    cos, sin = rope(cap, cfg, cuda)
+    kw = dict(seq_lens=lens, chunk_rows=128)
+    want = F.mla_decode(kv.to(torch.bfloat16), q_nope, q_rope, W_UK, W_UV, cos, sin, cfg, kernel_variant=2, **kw)
+    if paged:
+        bps = cap // bs
+        perm = torch.from_numpy(np.random.RandomState(114).permutation(B * bps).astype(np.int32)).to(cuda)
+        pool = torch.empty(B * cap, ROW, dtype=torch.float8_e4m3fn, device=cuda)
+        pool.view(torch.uint8).view(B * bps, bs, ROW)[perm.long()] = kv.view(torch.uint8).view(B * bps, bs, ROW)
+        got = F.mla_decode(pool, q_nope, q_rope, W_UK, W_UV, cos, sin, cfg, block_table=perm.view(B, bps),
+                           block_size=bs, **kw)
+    else:
+        got = F.mla_decode(kv, q_nope, q_rope, W_UK, W_UV, cos, sin, cfg, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), float((got - want).abs().max())
 
 
 def test_fp8_naive_matches_oracle(cuda):
