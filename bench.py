@@ -331,10 +331,16 @@ def measured_traffic(config: str):
         return None
 
 
-def cpu_baseline(inp, budget_s: float = 12.0):
-    """Time the oracle's absorbed float32 path (this repo's CPU restatement of
-    the reference math) on whole sequences of the workload, one at a time,
-    until ~budget_s; extrapolate to one step (all B sequences)."""
+def cpu_baseline(inp, budget_s: float = 10.0):
+    """CPU baseline on the box's host cores, two restatements of the
+    reference path from oracle/mla_oracle.py in float32, each on whole
+    sequences of the workload one at a time until ~budget_s, extrapolated by
+    positions to one step (all B sequences):
+      * value: the decompress-then-attend math of the reference's PyTorch
+        path (tests/test_python.py:26-63, oracle naive_mla): K_nope = c_t
+        W_UK^T and V = c_t W_UV^T materialised per sequence;
+      * absorbed: the reference kernel's algorithm (src/fused_mla.cu:218-267,
+        oracle absorb_q + absorbed_latent + project_wuv)."""
     import numpy as np
 
     from oracle import mla_oracle as mo
@@ -354,42 +360,195 @@ def cpu_baseline(inp, budget_s: float = 12.0):
     sin = inp["sin"].cpu().numpy()
     lens = [int(x) for x in inp["lens"]]
     offs = np.concatenate([[0], np.cumsum(lens)])
-    done_pos, done_seq, spent = 0, 0, 0.0
-    while spent < budget_s and done_seq < inp["B"]:
-        b = done_seq
-        kv = inp["kv"][offs[b]:offs[b + 1]].float().cpu().numpy()
-        qn = inp["q_nope"][b].cpu().numpy()
-        qr = inp["q_rope"][b].cpu().numpy()
-        t0 = time.perf_counter()
-        qa = mo.absorb_q(qn, W_UK, d, dtype=np.float32)
-        acc, _ = mo.absorbed_latent(kv, qa, qr, cos, sin, d, dtype=np.float32)
-        mo.project_wuv(acc, W_UV, d, dtype=np.float32)
-        spent += time.perf_counter() - t0
-        done_pos += lens[b]
-        done_seq += 1
     total_pos = int(sum(lens))
-    us_step = spent / done_pos * total_pos * 1e6
+
+    def run(kind):
+        done_pos, done_seq, spent = 0, 0, 0.0
+        while spent < budget_s and done_seq < inp["B"]:
+            b = done_seq
+            kv = inp["kv"][offs[b]:offs[b + 1]].float().cpu().numpy()
+            qn = inp["q_nope"][b].cpu().numpy()
+            qr = inp["q_rope"][b].cpu().numpy()
+            t0 = time.perf_counter()
+            if kind == "naive":
+                mo.naive_mla(kv, W_UK, W_UV, qn, qr, cos, sin, d, dtype=np.float32)
+            else:
+                qa = mo.absorb_q(qn, W_UK, d, dtype=np.float32)
+                acc, _ = mo.absorbed_latent(kv, qa, qr, cos, sin, d, dtype=np.float32)
+                mo.project_wuv(acc, W_UV, d, dtype=np.float32)
+            spent += time.perf_counter() - t0
+            done_pos += lens[b]
+            done_seq += 1
+        return spent / done_pos * total_pos * 1e6, done_seq, done_pos
+
+    naive_us, n_seq, n_pos = run("naive")
+    abs_us, a_seq, a_pos = run("absorbed")
     return {
-        "value": round(us_step, 1),
+        "value": round(naive_us, 1),
         "unit": "us/step",
         "cores": int(threads),
         "kind": "port",
-        "sample": f"{done_seq} of {inp['B']} sequences ({done_pos} positions) through oracle/mla_oracle.py "
-                  f"absorbed float32 path (absorb, latent attention, W_UV), extrapolated by positions",
+        "sample": f"{n_seq} of {inp['B']} sequences ({n_pos} positions) through oracle/mla_oracle.py naive_mla "
+                  f"(the reference's PyTorch decompress-then-attend math) in float32, extrapolated by positions",
+        "absorbed": {"value": round(abs_us, 1), "unit": "us/step",
+                     "sample": f"{a_seq} of {inp['B']} sequences ({a_pos} positions) through the absorbed "
+                               f"float32 path (absorb_q, absorbed_latent, project_wuv)"},
     }
+
+
+class Stepper:
+    """One decode step of a workload through la_mla_decode on `stream`, with
+    the workspace sized by la_mla_decode_workspace_size."""
+
+    def __init__(self, lib, capi, inp, stream, variant: int = 0):
+        import torch
+
+        self.lib, self.stream = lib, stream
+        cfg = inp["cfg"]
+        self.out = torch.empty(inp["B"], cfg.num_heads, cfg.v_head_dim, device=inp["kv"].device, dtype=torch.float32)
+        self.a = decode_args(inp, self.out, capi)
+        self.a.kernel_variant = variant
+        need = lib.la_mla_decode_workspace_size(ctypes.byref(self.a))
+        assert need > 0
+        self.ws = torch.empty(need, dtype=torch.uint8, device=inp["kv"].device)
+        self.a.workspace, self.a.workspace_bytes = self.ws.data_ptr(), need
+
+    def __call__(self, ev_b=None, ev_e=None, repeat=0):
+        a = self.a
+        a.decode_event_begin, a.decode_event_end, a.decode_repeat = ev_b, ev_e, repeat
+        st = self.lib.la_mla_decode(ctypes.byref(a), ctypes.c_void_p(self.stream))
+        if st != 0:
+            raise RuntimeError(f"la_mla_decode: {self.lib.la_status_string(st).decode()} "
+                               f"hip={self.lib.la_last_hip_error()}")
+
+
+def settle_clocks(step, min_ms: float) -> dict:
+    """Clock-settle phase, separate from --warmup: steps in batches of 20
+    until at least min_ms of wall time has passed with the GPU busy. The
+    MI355X's clocks take ~100 steps of this load to reach their loaded
+    steady state; timing before that reads up to ~20 % slow."""
+    import torch
+
+    n, t0 = 0, time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < min_ms:
+        for _ in range(20):
+            step()
+        torch.cuda.synchronize()
+        n += 20
+    return {"steps": n, "ms": round((time.perf_counter() - t0) * 1e3, 1)}
+
+
+def time_steps(hip, step, stream, K: int) -> float:
+    """Milliseconds per step over K back-to-back steps between one event pair."""
+    import torch
+
+    t0, t1 = new_event(hip), new_event(hip)
+    torch.cuda.synchronize()
+    hip.hipEventRecord(t0, ctypes.c_void_p(stream))
+    for _ in range(K):
+        step()
+    hip.hipEventRecord(t1, ctypes.c_void_p(stream))
+    hip.hipEventSynchronize(t1)
+    ms = elapsed_ms(hip, t0, t1) / K
+    hip.hipEventDestroy(t0)
+    hip.hipEventDestroy(t1)
+    return ms
+
+
+def time_attention(hip, step, calls: int = 10, repeat: int = 10) -> list:
+    """Attention-kernel milliseconds per launch: `calls` steps, each running
+    the attention kernel `repeat` times back to back (decode_repeat) between
+    one fence-free event pair on the launch stream. An event pair around a
+    single launch also times its dispatch (~5 us; in a step that dispatch
+    overlaps the previous kernel), while back-to-back launches overlap their
+    dispatches like the kernels of a step do, so the per-launch time agrees
+    with the profiler's kernel duration."""
+    import torch
+
+    evs = [(new_event(hip, True), new_event(hip, True)) for _ in range(calls)]
+    for b, e in evs:
+        step(b, e, repeat)
+    torch.cuda.synchronize()
+    ms = sorted(elapsed_ms(hip, b, e) / repeat for b, e in evs)
+    for b, e in evs:
+        hip.hipEventDestroy(b)
+        hip.hipEventDestroy(e)
+    return ms
+
+
+def time_mall_cold(hip, step, stream, dev, steps: int = 30, flush_mib: int = 1024) -> dict:
+    """Per-step times with one fence-free event pair around each step, once
+    with a device copy of flush_mib MiB between steps (it sweeps the 256 MB
+    infinity cache and every L2, so weights, queries, tables and the cache all
+    come from HBM: MALL-cold) and once back to back with the same events
+    (steady state). Both include the event pair's dispatch gap, so compare
+    them with each other, not with `value`."""
+    import torch
+
+    src = torch.empty(flush_mib << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    res = {}
+    for cold in (True, False):
+        evs = [(new_event(hip, True), new_event(hip, True)) for _ in range(steps)]
+        for b, e in evs:
+            if cold:
+                dst.copy_(src)
+            hip.hipEventRecord(b, ctypes.c_void_p(stream))
+            step()
+            hip.hipEventRecord(e, ctypes.c_void_p(stream))
+        torch.cuda.synchronize()
+        us = [elapsed_ms(hip, b, e) * 1e3 for b, e in evs]
+        for b, e in evs:
+            hip.hipEventDestroy(b)
+            hip.hipEventDestroy(e)
+        us.sort()
+        res["cold" if cold else "warm"] = {"mean_us": round(sum(us) / len(us), 2), "median_us": round(us[len(us) // 2], 2)}
+    del src, dst
+    return {"flush_mib": flush_mib, "steps": steps, **res}
+
+
+def config_leg(lib, capi, hip, name: str, dev, stream, steps: int = 50) -> dict:
+    """One configuration besides the headline one: microseconds per step,
+    tokens/s, the whole-step latent-cache rate, and the attention kernel's
+    time and fraction of 8 TB/s on its algorithmic cache bytes."""
+    import torch
+
+    inp = build_inputs(name, dev)
+    step = Stepper(lib, capi, inp, stream)
+    settle_clocks(step, 30)
+    ms = time_steps(hip, step, stream, steps)
+    kern = time_attention(hip, step)
+    kern_ms = sum(kern) / len(kern)
+    cache_bytes = int(inp["total"]) * BYTES_PER_POS
+    leg = {
+        "workload": CONFIGS[name]["desc"],
+        "total_positions": int(inp["total"]),
+        "step_us": round(ms * 1e3, 2),
+        "tokens_per_s": round(inp["B"] / (ms * 1e-3), 1),
+        "latent_cache_GBps": round(cache_bytes / (ms * 1e-3) / 1e9, 1),
+        "attn_kernel_us": round(kern_ms * 1e3, 2),
+        "attn_frac_of_8TBps": round(cache_bytes / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+    }
+    del step, inp
+    torch.cuda.empty_cache()
+    return leg
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # The GPU's clocks take ~100 decode steps (~15 ms) of load to settle: the
-    # default warmup covers that; 200 timed steps take ~30 ms.
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=200)
+    # Declared separately from --warmup: steps run for at least this long
+    # before the timed region so the GPU clocks reach their loaded state.
+    ap.add_argument("--settle-ms", type=float, default=200.0)
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--legs", default="cfg2,cfg4,cfg5",
+                    help="comma-separated other configurations timed after the headline one ('' for none)")
+    ap.add_argument("--no-mall-cold", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fp8", action="store_true",
-                    help="also time the step over an FP8 E4M3 copy of the cache (bf16 staging + MFMA attention kernel)")
+                    help="also time the step over an FP8 E4M3 copy of the cache")
     ap.add_argument("--layer", action="store_true",
                     help="also time LatentAttentionLayer.forward_batch (fp32 projections, 1.8 GB of weights) "
                          "on the same batch and cache")
@@ -423,77 +582,46 @@ def main():
     inp = build_inputs(args.config, device)
     cfg = inp["cfg"]
     B = inp["B"]
-    out = torch.empty(B, cfg.num_heads, cfg.v_head_dim, device=device, dtype=torch.float32)
-    a = decode_args(inp, out, capi)
-    a.kernel_variant = args.variant
-    ws_bytes = lib.la_mla_decode_workspace_size(ctypes.byref(a))
-    assert ws_bytes > 0
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
-    a.workspace = ws.data_ptr()
-    a.workspace_bytes = ws_bytes
     stream = torch.cuda.current_stream().cuda_stream
+    step = Stepper(lib, capi, inp, stream, args.variant)
     torch.cuda.synchronize()
-
-    def step(ev_b=None, ev_e=None, repeat=0):
-        a.decode_event_begin = ev_b
-        a.decode_event_end = ev_e
-        a.decode_repeat = repeat
-        st = lib.la_mla_decode(ctypes.byref(a), ctypes.c_void_p(stream))
-        if st != 0:
-            raise RuntimeError(f"la_mla_decode: {lib.la_status_string(st).decode()} hip={lib.la_last_hip_error()}")
 
     log(f"[bench] warmup {args.warmup}")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    log(f"[bench] clock settle {args.settle_ms} ms")
+    settle = settle_clocks(step, args.settle_ms)
 
     K = args.steps
-    # attention-kernel timing: KERN_CALLS steps, each launching the kernel
-    # KERN_REPEAT times back to back between one event pair
-    KERN_CALLS, KERN_REPEAT = 10, 10
-    evs = [(new_event(hip, True), new_event(hip, True)) for _ in range(KERN_CALLS)]
-    t_start, t_end = new_event(hip), new_event(hip)
     log(f"[bench] timing {K} steps")
-    torch.cuda.synchronize()
-    hip.hipEventRecord(t_start, ctypes.c_void_p(stream))
-    for i in range(K):
-        step()
-    hip.hipEventRecord(t_end, ctypes.c_void_p(stream))
-    hip.hipEventSynchronize(t_end)
-    torch.cuda.synchronize()
-    ms_total = elapsed_ms(hip, t_start, t_end)
-    # Attention-kernel time: KERN_CALLS more steps, each running the attention
-    # kernel KERN_REPEAT times back to back (decode_repeat) between one
-    # fence-free event pair on the launch stream. An event pair around a
-    # single launch also times its dispatch (~5 us here; in a step that
-    # dispatch overlaps the previous kernel), while back-to-back launches of
-    # the kernel overlap their dispatches like the kernels of a step do, so
-    # the per-launch time agrees with the profiler's kernel duration. Events
-    # stay out of the step time above.
-    log(f"[bench] timing the attention kernel: {KERN_CALLS} x {KERN_REPEAT} launches")
-    for i in range(KERN_CALLS):
-        step(evs[i][0], evs[i][1], KERN_REPEAT)
-    torch.cuda.synchronize()
-    kern_ms = sorted(elapsed_ms(hip, b, e) / KERN_REPEAT for b, e in evs)
-    kern_avg = sum(kern_ms) / KERN_CALLS
-    ms_step = ms_total / K
+    ms_step = time_steps(hip, step, stream, K)
+    log("[bench] timing the attention kernel: 10 x 10 launches")
+    kern_ms = time_attention(hip, step)
+    kern_avg = sum(kern_ms) / len(kern_ms)
     us_step = ms_step * 1e3
+    log("[bench] append / paged legs")
     append_us = time_append(lib, hip, capi, inp, stream)
-    paged = time_paged(lib, hip, capi, inp, out, ws, stream) if inp["offsets"] is None else None
+    paged = time_paged(lib, hip, capi, inp, step.out, step.ws, stream) if inp["offsets"] is None else None
     layer = time_layer(hip, inp, stream) if args.layer else None
-    fp8 = time_fp8(lib, hip, capi, inp, out, stream) if args.fp8 else None
+    fp8 = time_fp8(lib, hip, capi, inp, step.out, stream) if args.fp8 else None
+    mall = None
+    if not args.no_mall_cold:
+        log("[bench] MALL-cold leg")
+        mall = time_mall_cold(hip, step, stream, device)
 
     total_pos = int(inp["total"])
     cache_bytes = total_pos * BYTES_PER_POS
     flops_attn = total_pos * 2 * cfg.num_heads * (cfg.kv_lora_rank + cfg.qk_rope_head_dim + cfg.kv_lora_rank)
     achieved_gbps = cache_bytes / (kern_avg * 1e-3) / 1e9
     line = {
-        "metric": "\u00b5s/decode step + achieved latent-cache HBM GB/s, H=128 d_c=512, B=32 seq=8K",
+        "metric": "µs/decode step + achieved latent-cache HBM GB/s, H=128 d_c=512, B=32 seq=8K",
         "value": round(us_step, 2),
         "unit": "us/step",
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
+        "clock_settle": settle,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": False,
         "scaling": "weak",
@@ -519,6 +647,7 @@ def main():
         "mfma_frac_of_bf16_peak": round(flops_attn / (kern_avg * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         "append_kernel_us": round(append_us, 2),
         **({"paged_block64": paged} if paged else {}),
+        **({"mall_cold": mall} if mall else {}),
         **({"layer_forward_batch": layer} if layer else {}),
         **({"fp8_cache": fp8} if fp8 else {}),
         "roofline": {
@@ -530,9 +659,15 @@ def main():
             "traffic": measured_traffic(args.config),
         },
     }
-    for b, e in evs:
-        hip.hipEventDestroy(b)
-        hip.hipEventDestroy(e)
+    legs = [c for c in args.legs.split(",") if c and c != args.config]
+    if legs:
+        del step, inp
+        torch.cuda.empty_cache()
+        line["other_configs"] = {}
+        for c in legs:
+            log(f"[bench] leg {c}")
+            line["other_configs"][c] = config_leg(lib, capi, hip, c, device, stream)
+        inp = build_inputs(args.config, device) if not args.no_cpu_baseline else None
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
         line["cpu_baseline"] = cpu_baseline(inp)

@@ -243,8 +243,13 @@ int la_batched_fused_mla(const void* kv_cache, int kv_dtype, int seq_len, int ba
                          size_t workspace_bytes, void* stream);
 
 /* Workspace bytes la_fused_mla / la_batched_fused_mla need (batch_size 1 for
- * la_fused_mla). */
+ * la_fused_mla): the largest over every cache and weight dtype. */
 size_t la_fused_mla_workspace_size(int seq_len, int batch_size, const la_mla_config* cfg);
+
+/* The same for one cache / weight dtype pair (la_dtype values): what the
+ * torch extension and the C++ drop-in allocate. */
+size_t la_fused_mla_workspace_size_dt(int seq_len, int batch_size, const la_mla_config* cfg, int kv_dtype,
+                                      int w_uv_dtype);
 
 /* Decompress-then-attend on the GPU, the reference's naive path
  * (naive_mla_forward, csrc/bindings.cpp:53-114; math of

@@ -6,6 +6,9 @@
 * ``latent_attn/_C<ext>`` -- the PyTorch-ROCm extension (pybind11) that wraps
   the C ABI; host-only C++ compiled with g++ against torch's headers and
   linked to the library with an $ORIGIN rpath.
+* ``tests/cpp/reference_caller`` -- the C++ drop-in test program (a caller
+  of include/fused_mla.hpp written like the reference's C++ test), run by
+  tests/test_gpu_cpp_caller.py.
 
 Usage: ``python latent-attn_amd/build.py [--lib-only]``. Always recompiles.
 """
@@ -98,10 +101,22 @@ def build_ext() -> str:
     return out
 
 
+def build_cpp_caller() -> str:
+    src = os.path.join(ROOT, "tests", "cpp", "reference_caller.cpp")
+    out = os.path.join(ROOT, "tests", "cpp", "reference_caller")
+    tmp = out + ".tmp"
+    _run([HIPCC, "-x", "hip", "--offload-arch=gfx950", "-std=c++17", "-O2", "-Wno-implicit-const-int-float-conversion",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", f"-I{INC}", src, "-o", tmp, f"-L{PKG}",
+          "-llatent_attn_hip", "-Wl,-rpath,$ORIGIN/../../latent-attn_amd/latent_attn"])
+    os.replace(tmp, out)
+    return out
+
+
 def build(lib_only: bool = False) -> None:
     build_lib()
     if not lib_only:
         build_ext()
+        build_cpp_caller()
 
 
 if __name__ == "__main__":

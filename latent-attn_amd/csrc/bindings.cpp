@@ -109,7 +109,7 @@ torch::Tensor fused_mla_forward(torch::Tensor kv_cache, torch::Tensor q_absorbed
 
   const at::DeviceGuard guard(kv_cache.device());
   auto output = torch::empty({num_heads, v_head_dim}, kv_cache.options().dtype(torch::kFloat32));
-  const size_t ws_bytes = la_fused_mla_workspace_size((int)seq_len, 1, &cfg);
+  const size_t ws_bytes = la_fused_mla_workspace_size_dt((int)seq_len, 1, &cfg, dtype_tag(kv_cache), dtype_tag(W_UV));
   auto ws = workspace(kv_cache, ws_bytes);
   int st = la_fused_mla(kv_cache.data_ptr(), dtype_tag(kv_cache), (int)seq_len, q_absorbed.data_ptr<float>(),
                         q_rope.data_ptr<float>(), W_UV.data_ptr(), dtype_tag(W_UV), rope_cos.data_ptr<float>(),
@@ -155,7 +155,8 @@ torch::Tensor batched_fused_mla_forward(torch::Tensor kv_cache, torch::Tensor q_
 
   const at::DeviceGuard guard(kv_cache.device());
   auto output = torch::empty({batch, num_heads, v_head_dim}, kv_cache.options().dtype(torch::kFloat32));
-  const size_t ws_bytes = la_fused_mla_workspace_size((int)seq_len, (int)batch, &cfg);
+  const size_t ws_bytes =
+      la_fused_mla_workspace_size_dt((int)seq_len, (int)batch, &cfg, dtype_tag(kv_cache), dtype_tag(W_UV));
   auto ws = workspace(kv_cache, ws_bytes);
   int st = la_batched_fused_mla(kv_cache.data_ptr(), dtype_tag(kv_cache), (int)seq_len, (int)batch,
                                 q_absorbed.data_ptr<float>(), q_rope.data_ptr<float>(), W_UV.data_ptr(),
@@ -205,6 +206,7 @@ torch::Tensor run_decode(la_decode_args& a, const torch::Tensor& kv_cache, const
     TORCH_CHECK(seq_lens.has_value() && seq_lens->defined(), "a paged cache needs seq_lens");
     TORCH_CHECK(block_size > 0 && kv_cache.dim() == 2 && kv_cache.size(1) == row && kv_cache.size(0) % block_size == 0,
                 "paged kv_cache must be a (num_blocks * block_size, ", row, ") pool");
+    TORCH_CHECK(batch == 0 || kv_cache.size(0) >= block_size, "paged kv_cache pool needs at least one block");
     check_same_device(kv_cache, bt, "block_table");
     a.total_rows = kv_cache.size(0);
     a.block_table = bt.data_ptr<int32_t>();
@@ -373,6 +375,7 @@ void append_kv_forward(torch::Tensor kv_cache, torch::Tensor seq_lens, torch::Te
     TORCH_CHECK(!(seq_offsets.has_value() && seq_offsets->defined()), "block_table and seq_offsets exclude each other");
     TORCH_CHECK(block_size > 0 && kv_cache.dim() == 2 && kv_cache.size(1) == row && kv_cache.size(0) % block_size == 0,
                 "paged kv_cache must be a (num_blocks * block_size, ", row, ") pool");
+    TORCH_CHECK(batch == 0 || kv_cache.size(0) >= block_size, "paged kv_cache pool needs at least one block");
     check_same_device(kv_cache, bt, "block_table");
     a.total_rows = kv_cache.size(0);
     a.block_table = bt.data_ptr<int32_t>();

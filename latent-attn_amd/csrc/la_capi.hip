@@ -83,7 +83,8 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
     // blocks_per_seq blocks whose filled length comes from seq_lens
     if (a->block_size <= 0 || a->blocks_per_seq <= 0 || a->seq_offsets || !a->seq_lens ||
         a->total_rows % a->block_size != 0 || (int64_t)a->blocks_per_seq * a->block_size > INT32_MAX ||
-        a->total_rows > (int64_t)UINT32_MAX)  // pool rows are 32-bit in the MFMA kernel
+        a->total_rows > (int64_t)UINT32_MAX ||  // pool rows are 32-bit in the MFMA kernel
+        (a->num_seqs > 0 && a->total_rows < a->block_size))  // a pool without a block: nothing to clamp into
       return LA_ERROR_INVALID_VALUE;
   } else if (!a->seq_offsets && (a->seq_len < 0 || (int64_t)a->num_seqs * a->seq_len > a->total_rows)) {
     return LA_ERROR_INVALID_VALUE;
@@ -382,24 +383,31 @@ int la_batched_fused_mla(const void* kv_cache, int kv_dtype, int seq_len, int ba
   return la::run(&a, static_cast<hipStream_t>(stream));
 }
 
-size_t la_fused_mla_workspace_size(int seq_len, int batch_size, const la_mla_config* cfg) {
+size_t la_fused_mla_workspace_size_dt(int seq_len, int batch_size, const la_mla_config* cfg, int kv_dtype,
+                                      int w_uv_dtype) {
   if (!cfg || seq_len < 0 || batch_size <= 0) return 0;
-  // Only plan-relevant fields are read. The kernel family is not known here
-  // (it depends on dtype and pointer alignment), so return the larger of the
-  // plans (an fp8 cache's includes its bf16 staging copy).
+  // Only plan-relevant fields are read. Which kernel family runs also depends
+  // on pointer alignment, so return the larger of the two families' plans.
   alignas(256) static const char dummy[256] = {0};
   const float* d = reinterpret_cast<const float*>(dummy);
   size_t best = 0;
   for (int variant : {1, 2}) {
-    for (int dt : {LA_DTYPE_F16, LA_DTYPE_F32, LA_DTYPE_FP8_E4M3}) {
-      la_decode_args a = la::shared_cache_args(dummy, dt, seq_len, batch_size, d, d, dummy, dt, d, d,
-                                               const_cast<float*>(d), cfg, nullptr, 0);
-      a.kernel_variant = variant;
-      la::DecodeProblem p;
-      la::Plan plan;
-      if (la::prepare(&a, &p, &plan) == LA_SUCCESS && plan.total > best) best = plan.total;
-    }
+    la_decode_args a = la::shared_cache_args(dummy, kv_dtype, seq_len, batch_size, d, d, dummy, w_uv_dtype, d, d,
+                                             const_cast<float*>(d), cfg, nullptr, 0);
+    a.kernel_variant = variant;
+    la::DecodeProblem p;
+    la::Plan plan;
+    if (la::prepare(&a, &p, &plan) == LA_SUCCESS && plan.total > best) best = plan.total;
   }
+  return best;
+}
+
+size_t la_fused_mla_workspace_size(int seq_len, int batch_size, const la_mla_config* cfg) {
+  // every cache dtype with every weight dtype
+  size_t best = 0;
+  for (int kv : {LA_DTYPE_F16, LA_DTYPE_BF16, LA_DTYPE_F32, LA_DTYPE_FP8_E4M3})
+    for (int w : {LA_DTYPE_F16, LA_DTYPE_BF16, LA_DTYPE_F32})
+      best = std::max(best, la_fused_mla_workspace_size_dt(seq_len, batch_size, cfg, kv, w));
   return best;
 }
 
@@ -462,7 +470,8 @@ int la_append_kv(const la_append_args* a, void* stream) {
   if (a->num_seqs < 0 || a->tokens_per_seq < 0 || a->total_rows < 0 || a->rope_rows < 0) return LA_ERROR_INVALID_VALUE;
   const bool paged = a->block_table != nullptr;
   if (paged) {
-    if (a->block_size <= 0 || a->blocks_per_seq <= 0 || a->seq_offsets || a->total_rows % a->block_size != 0)
+    if (a->block_size <= 0 || a->blocks_per_seq <= 0 || a->seq_offsets || a->total_rows % a->block_size != 0 ||
+        (a->num_seqs > 0 && a->total_rows < a->block_size))  // a pool without a block: nothing to clamp into
       return LA_ERROR_INVALID_VALUE;
   } else if (!a->seq_offsets && (a->seq_capacity < 0 || (int64_t)a->num_seqs * a->seq_capacity > a->total_rows)) {
     return LA_ERROR_INVALID_VALUE;

@@ -73,9 +73,10 @@ def naive_mla(
 ) -> torch.Tensor:
     """Single-token MLA forward from the un-absorbed query (q_nope, W_UK).
 
-    Returns the decompress-then-attend result (num_heads, v_head_dim) fp32. It
-    is computed on the GPU by absorbing q_nope into the latent space and
-    running the fused decode (the same function of the inputs).
+    Returns the decompress-then-attend result (num_heads, v_head_dim) fp32,
+    computed on the GPU by la_naive_mla: K_nope = c_t W_UK^T and V = c_t
+    W_UV^T materialised in fp32, RoPE on k_rope, softmax, P V -- independent
+    of the absorbed kernels (reference tests/test_python.py:26-63).
     """
     _C = _load_ext()
     return _C.naive_mla_forward(kv_cache, W_UK, W_UV, q_nope, q_rope, rope_cos, rope_sin, *_cfg_args(cfg))

@@ -42,8 +42,28 @@ BF16_ATOL, BF16_RTOL, BF16_NORM = 2e-2, 1e-2, 1e-2
 FP32_ATOL, FP32_RTOL, FP32_NORM = 1e-4, 1e-4, 1e-5
 
 
+# Achieved margins of every assert_close call in this session: (what, dtype,
+# max abs, floored max rel, normwise, cosine). With LA_MARGINS_FILE set, the
+# session writes them there as JSON lines.
+MARGINS: list = []
+
+
+def pytest_sessionfinish(session, exitstatus):
+    path = os.environ.get("LA_MARGINS_FILE")
+    if path and MARGINS:
+        import json
+
+        with open(path, "w") as f:
+            for m in MARGINS:
+                f.write(json.dumps(m) + "\n")
+
+
 def assert_close(out, ref, dtype: str, what: str = ""):
-    from oracle.mla_oracle import norm_rel_err
+    """Elementwise |d| <= atol + rtol*|ref| and normwise ||d|| / ||ref|| <=
+    norm; also computes (and records in MARGINS) the floored max-rel
+    |d| / max(|ref|, 1e-3 max|ref|) and the cosine, which are reported, not
+    gated. Returns the margins as a dict."""
+    from oracle.mla_oracle import max_rel_err, norm_rel_err
 
     out = np.asarray(out, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
@@ -56,6 +76,19 @@ def assert_close(out, ref, dtype: str, what: str = ""):
     d = np.abs(out - ref)
     bad = d > atol + rtol * np.abs(ref)
     ne = norm_rel_err(out, ref)
+    den = np.linalg.norm(out) * np.linalg.norm(ref)
+    m = {
+        "what": what,
+        "dtype": dtype,
+        "max_abs": float(d.max()) if d.size else 0.0,
+        "max_rel_floored": max_rel_err(out, ref),
+        "norm_rel": ne,
+        "cosine": float((out * ref).sum() / den) if den > 0 else 1.0,
+        "max_abs_ref": float(np.abs(ref).max()) if ref.size else 0.0,
+    }
+    MARGINS.append(m)
+    print(f"[margins] {what}: max_abs {m['max_abs']:.3e} max_rel(floored) {m['max_rel_floored']:.3e} "
+          f"norm {ne:.3e} cos {m['cosine']:.7f} (max|ref| {m['max_abs_ref']:.3e})")
     assert not bad.any(), f"{what}: {bad.sum()} elements outside atol={atol} rtol={rtol}; max abs {d.max():.3e}"
     assert ne <= nrm, f"{what}: normwise relative error {ne:.3e} > {nrm}"
-    return ne
+    return m

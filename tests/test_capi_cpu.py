@@ -256,6 +256,18 @@ def test_cpp_dropin_header_compiles_and_links(tmp_path):
         "                                      nullptr, &cfg};\n"
         "  if (p.kv_dtype != LA_DTYPE_F16 || b.batch_size != 2) return 2;\n"
         "  if (latent_attn::launch_fused_mla(latent_attn::FusedMLAParams{}) != hipErrorInvalidValue) return 3;\n"
+        "  // the reference's names without a qualifier (src/fused_mla.cuh, src/mla_config.cuh)\n"
+        "  MLAConfig c2 = MLAConfig::deepseek_v3();\n"
+        "  FusedMLAParams q; q.cfg = nullptr;\n"
+        "  if (launch_fused_mla(q) != hipErrorInvalidValue) return 4;\n"
+        "  BatchedFusedMLAParams bq; bq.cfg = &c2; bq.batch_size = 0;\n"
+        "  __half* base = reinterpret_cast<__half*>(0x1000);\n"
+        "  LatentKVCache cache(base, 4, c2);\n"
+        "  if (cache.entry_stride != 576 || cache.current_len != 0 || cache.row(2) != base + 2 * 576) return 5;\n"
+        "  // one dtype pair never needs more than the largest over all pairs\n"
+        "  const la_mla_config cc = c2.c_abi();\n"
+        "  if (fused_mla_workspace_size(16, 2, c2, LA_DTYPE_BF16, LA_DTYPE_BF16) >\n"
+        "      la_fused_mla_workspace_size(16, 2, &cc)) return 6;\n"
         "  return latent_attn::fused_mla_workspace_size(16, 2, cfg) > 0 ? 0 : 1;\n"
         "}\n")
     libdir = os.path.join(REPO, "latent-attn_amd", "latent_attn")
@@ -291,6 +303,7 @@ def test_naive_rejects_bad_arguments_and_sizes_its_workspace():
     ("seq_lens", 0),            # a paged cache needs device lengths
     ("seq_offsets", 0x3000),    # block tables and packed offsets exclude each other
     ("total_rows", 100),        # the pool is whole blocks
+    ("total_rows", 0),          # a pool without a block: no row to clamp a table entry into
 ])
 def test_decode_rejects_bad_paged_arguments(field, value):
     lib = capi.load()
@@ -301,7 +314,8 @@ def test_decode_rejects_bad_paged_arguments(field, value):
 
 def test_append_rejects_bad_paged_arguments():
     lib = capi.load()
-    for field, value in (("block_size", 0), ("blocks_per_seq", -1), ("seq_offsets", 0x3000), ("total_rows", 100)):
+    for field, value in (("block_size", 0), ("blocks_per_seq", -1), ("seq_offsets", 0x3000), ("total_rows", 100),
+                         ("total_rows", 0)):
         a = _append_args(block_table=0x2000, block_size=64, blocks_per_seq=2, total_rows=256)
         setattr(a, field, value)
         assert lib.la_append_kv(ctypes.byref(a), None) == capi.LA_ERROR_INVALID_VALUE, field

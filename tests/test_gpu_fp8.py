@@ -127,3 +127,29 @@ def test_fp8_append_encodes_like_the_oracle(cuda):
     assert np.array_equal(p[3 * 32:3 * 32 + T], want[0])          # sequence 0, block 0 -> pool block 3
     assert np.array_equal(p[1 * 32 + 10:1 * 32 + 10 + T], want[1])  # sequence 1, block 0 -> pool block 1
     assert lens.cpu().tolist() == [T, 10 + T] == lens_p.cpu().tolist()
+
+
+@pytest.mark.parametrize("batched", [False, True])
+def test_fp8_fused_entries_match_oracle(cuda, batched):
+    """fused_mla_forward / batched_fused_mla_forward (the reference's
+    bindings, csrc/bindings.cpp:126-244) over an fp8 cache with bf16 W_UV:
+    the workspace they size for that dtype pair must be enough, and the
+    result matches the oracle at the bf16 tolerance."""
+    cfg = MLAConfig.deepseek_v2()
+    S, B = 700, 3
+    kv = fp8_cache((S, ROW), 121, cuda)
+    _, W_UV = make_weights(cfg, "bf16", 122, cuda)
+    g = torch.Generator().manual_seed(123)
+    lead = (B,) if batched else ()
+    qa = (torch.randn(*lead, 128, 512, generator=g) * 0.5).to(cuda)
+    qr = torch.randn(*lead, 128, 64, generator=g).to(cuda)
+    cos, sin = rope(S, cfg, cuda)
+    fn = F.batched_fused_mla if batched else F.fused_mla
+    out = fn(kv, qa, qr, W_UV, cos, sin, cfg)
+    torch.cuda.synchronize()
+    kv_np = fp8_np(kv)
+    if batched:
+        ref = mo.batched_absorbed_mla(kv_np, to_np(qa), to_np(qr), to_np(W_UV), to_np(cos), to_np(sin), D)
+    else:
+        ref = mo.absorbed_mla(kv_np, to_np(qa), to_np(qr), to_np(W_UV), to_np(cos), to_np(sin), D)
+    assert_close(out.cpu().numpy(), ref, "bf16", f"fp8 fused batched={batched}")

@@ -272,3 +272,22 @@ def test_capi_multi_query_absorb(cuda, heads, qps, variant):
             acc, _ = mo.absorbed_latent(kvn[offs[s_]:offs[s_ + 1]], qa, qr[t], to_np(cos), to_np(sin), d)
             ref[t] = mo.project_wuv(acc, wv, d)
     assert_close(out.cpu().numpy(), ref, "bf16", f"heads {heads} qps {qps} variant {variant}")
+
+
+@pytest.mark.parametrize("wdtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("tokens", [1, 37])
+def test_absorb_q_matches_oracle(cuda, wdtype, tokens):
+    """la_absorb_q (F.absorb_q) against the oracle's absorption (reference
+    tests/test_correctness.cu:29-46): the MFMA kernel for 16-bit weights
+    (q_nope split into 16-bit high and low parts) and the VALU kernel for
+    fp32 weights, at the fp32 tolerance; 37 tokens leave a partial 32-token
+    block."""
+    cfg = MLAConfig.deepseek_v2()
+    W_UK, _ = make_weights(cfg, wdtype, 131, cuda)
+    g = torch.Generator().manual_seed(132)
+    q_nope = torch.randn(tokens, 128, 128, generator=g).to(cuda)
+    out = F.absorb_q(q_nope, W_UK, cfg)
+    torch.cuda.synchronize()
+    ref = mo.absorb_q(to_np(q_nope), to_np(W_UK), dims(cfg))
+    assert out.shape == (tokens, 128, 512) and out.dtype == torch.float32
+    assert_close(out.cpu().numpy(), ref, "f32", f"absorb_q {wdtype} x{tokens}")
