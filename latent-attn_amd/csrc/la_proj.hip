@@ -247,16 +247,30 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
 // combine + project
 // ---------------------------------------------------------------------------
 constexpr int kDcP = 512;
+constexpr int kMPRows = 16;  // query rows per merge + projection workgroup
 
-// merge: one wave per (query row r, weight head h). o_merged[r][h][:] =
-// sum_slots 2^(lse_s - m) * part_o_s / sum_slots 2^(lse_s - m), m = max lse
-// (reference has no split; the merge is exact in real arithmetic). Lane l owns
-// latent columns 8l .. 8l+7; the slot loads go out 8 at a time.
-constexpr int kMergeWaves = 4;
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+template <typename WT>
+struct Mma16;
+template <>
+struct Mma16<__hip_bfloat16> {
+  typedef bf16x8 vec;
+  static __device__ inline f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mma16<__half> {
+  typedef f16x8 vec;
+  static __device__ inline f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
 
 // One slot's 8 columns of this lane, kept in the stored format until use
-// (fp16 rows: before the row scale, which the caller folds into the slot
-// weight), so 8 slots in flight cost 32 VGPRs for fp16 rows.
+// (fp16 numerator rows: before their row scale, which the slot weight
+// carries), so 8 slots in flight cost 32 VGPRs for fp16 rows.
 template <bool F16>
 struct SlotRow;
 template <>
@@ -284,167 +298,229 @@ struct SlotRow<false> {
   }
 };
 
-// F16: partial rows are fp16 numerators with a power-of-two scale per half row
-// (part_scale) and the running max of their scores (part_m).
-template <bool F16>
-__global__ __launch_bounds__(kMergeWaves * 64) void merge_slots_kernel(DecodeProblem p, float* __restrict__ o_merged) {
-  typedef typename std::conditional<F16, _Float16, float>::type PT;
-  const int lane = threadIdx.x & 63;
-  const int R = p.num_seqs * p.qps;
-  const int Rp = (R + 31) & ~31;  // rows padded to the projection's 32-row blocks
-  // wave -> (weight head h, query row r), r fastest: the waves of a block write
-  // neighbouring rows, which share the 128-B lines of the operand-order output
-  const int64_t pair = (int64_t)blockIdx.x * kMergeWaves + (threadIdx.x >> 6);
-  if (pair >= (int64_t)Rp * p.nh) return;
-  const int h = (int)(pair / Rp), r = (int)(pair % Rp);
-  if (r >= R) return;
-  const int s = r / p.qps;
-  const int hq = (r % p.qps) * p.nh + h;
-  f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
+// Log-sum-exp merge of split partial slots:
+//   O = sum_s 2^(lse_s - M) (O/l)_s / sum_s 2^(lse_s - M),  M = max_s lse_s.
+// F16 (MFMA attention kernel): slot rows hold the numerator N_s = sum 2^(s-m_s) V
+// as fp16 N_s 2^-e per half row, so (O/l)_s 2^(lse_s - M) = N_s 2^(m_s - M) 2^e.
+// F32 (VALU attention kernel): slot rows hold O/l in fp32.
+//
+// A merge task is (query row t, slot group g of G): it adds the slots
+// s = g, g + G, g + 2G, ... of row t, each weighted and divided by the sum
+// over ALL slots of the row, into this lane's 8 latent columns 8 lane ..
+// 8 lane + 7 (one wave per task), so the G tasks of a row sum to its merged O.
+// Rows past the batch and empty sequences give 0.
+struct MergeTask {
+  int n = 0;       // slots of the row
+  int ns = 0;      // slots of this task (g, g + G, ...)
+  int64_t row0 = 0;  // partial row of the row's first slot
+};
+
+__device__ inline MergeTask merge_task(const DecodeProblem& p, int t, int h, int g, int G) {
+  MergeTask m;
+  if (t < 0 || t >= p.num_seqs * p.qps) return m;
+  const int s = t / p.qps;
+  const int hq = (t % p.qps) * p.nh + h;
   const int64_t lo = seq_begin(p, s), hi = seq_end(p, s);
-  if (hi > lo) {
-    const int64_t cf = lo / p.chunk_len;
-    const int n = (int)((hi - 1) / p.chunk_len - cf + 1);  // slots cf+s .. cf+s+n-1
-    const int64_t row0 = (cf + s) * p.Hq + hq;
-    const float* lse = p.part_lse + row0;
-    const PT* src = reinterpret_cast<const PT*>(p.part_o) + row0 * kDcP + 8 * lane;
-    const int64_t sstride = (int64_t)p.Hq * kDcP;
-    // The first 8 slot rows go out before the log-sum-exps they are weighted
-    // by, so a merge of up to 8 slots takes one memory round trip.
-    SlotRow<F16> d[8];
+  if (hi <= lo) return m;
+  const int64_t cf = lo / p.chunk_len;
+  m.n = (int)((hi - 1) / p.chunk_len - cf + 1);  // slots cf+s .. cf+s+n-1
+  m.ns = m.n > g ? (m.n - g + G - 1) / G : 0;
+  m.row0 = (cf + s) * p.Hq + hq;
+  return m;
+}
+
+// Merges up to two tasks (t[1] < 0: one) of the same slot group g of G.
+// Every load of both tasks goes out before anything waits: the first 8 slot
+// rows of each task, each row's log-sum-exps (lane i: slot i, for the
+// maximum and the denominator) and the weights' inputs of the task's own
+// slots (lane i: slot g + G i), so a merge of up to 8 own slots out of at
+// most 64 takes one memory round trip. Longer merges loop over further
+// groups of 8 rows (and of 64 slots). Lane i's weights are broadcast with
+// v_readlane.
+template <bool F16>
+__device__ inline void merge_tasks(const DecodeProblem& p, const int (&t)[2], int h, int g, int G, int lane,
+                                   f32x4 (&o)[2][2]) {
+  typedef typename std::conditional<F16, _Float16, float>::type PT;
+  const int64_t sstride = (int64_t)p.Hq * kDcP;
+  MergeTask mt[2];
+  const PT* src[2];
+  SlotRow<F16> d[2][8];
+  float ls_all[2], ls_own[2], m_own[2], sa_own[2], sb_own[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    mt[k] = merge_task(p, t[k], h, g, G);
+    src[k] = reinterpret_cast<const PT*>(p.part_o) + mt[k].row0 * kDcP + 8 * lane;
 #pragma unroll
     for (int u = 0; u < 8; ++u)
-      if (u < n) d[u].load(src + (int64_t)u * sstride);
-    // Lane i holds slot i of each 64-slot chunk (chunk 0 stays in registers).
-    // Denominator weight 2^(lse - M); numerator weight 2^(lse - M) for fp32
-    // O / l rows, 2^(m - M) * 2^e(half) for fp16 numerator rows (lanes 0..31
-    // hold columns 0..255, half 0).
-    const float ls0 = lane < n ? lse[(int64_t)lane * p.Hq] : -INFINITY;
-    float mm0 = 0.f, sa0 = 1.f, sb0 = 1.f;
+      if (u < mt[k].ns) d[k][u].load(src[k] + (int64_t)(g + G * u) * sstride);
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const float* lse = p.part_lse + mt[k].row0;
+    ls_all[k] = lane < mt[k].n ? lse[(int64_t)lane * p.Hq] : -INFINITY;
+    const bool own = lane < mt[k].ns;
+    const int64_t pr = mt[k].row0 + (int64_t)(g + G * (own ? lane : 0)) * p.Hq;
+    ls_own[k] = own ? p.part_lse[pr] : -INFINITY;
     if constexpr (F16) {
-      if (lane < n) {
-        const int64_t pr = row0 + (int64_t)lane * p.Hq;
-        mm0 = p.part_m[pr];
-        sa0 = p.part_scale[2 * pr];
-        sb0 = p.part_scale[2 * pr + 1];
-      }
+      m_own[k] = own ? p.part_m[pr] : -INFINITY;
+      sa_own[k] = own ? p.part_scale[2 * pr] : 0.f;
+      sb_own[k] = own ? p.part_scale[2 * pr + 1] : 0.f;
     }
-    float mx = ls0;
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    o[k][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    o[k][1] = o[k][0];
+    const int n = mt[k].n, ns = mt[k].ns;
+    if (n == 0) continue;  // wave-uniform
+    const float* lse = p.part_lse + mt[k].row0;
+    // M and the denominator over every slot of the row
+    float mx = ls_all[k];
     for (int i = lane + 64; i < n; i += 64) mx = fmaxf(mx, lse[(int64_t)i * p.Hq]);
     mx = wave_max(mx);
-    float wsum = 0.f;
-    for (int i0 = 0; i0 < n; i0 += 64) {
-      const int nb = min(64, n - i0);
-      float ls = ls0, mm = mm0, sa = sa0, sb = sb0;
+    float den = lane < n ? exp2f(ls_all[k] - mx) : 0.f;
+    for (int i = lane + 64; i < n; i += 64) den += exp2f(lse[(int64_t)i * p.Hq] - mx);
+    const float inv = 1.f / wave_sum(den);
+    for (int i0 = 0; i0 < ns; i0 += 64) {
+      const int nb = min(64, ns - i0);
+      // this lane's slot: g + G (i0 + lane)
+      float ls = ls_own[k], mm = m_own[k], sa = sa_own[k], sb = sb_own[k];
       if (i0 > 0) {
         const bool ok = lane < nb;
-        const int64_t pr = row0 + (int64_t)(min(i0 + lane, n - 1)) * p.Hq;
-        ls = ok ? lse[(int64_t)(i0 + lane) * p.Hq] : -INFINITY;
+        const int64_t pr = mt[k].row0 + (int64_t)(g + G * (i0 + (ok ? lane : 0))) * p.Hq;
+        ls = ok ? p.part_lse[pr] : -INFINITY;
         if constexpr (F16) {
-          mm = ok ? p.part_m[pr] : 0.f;
-          sa = ok ? p.part_scale[2 * pr] : 1.f;
-          sb = ok ? p.part_scale[2 * pr + 1] : 1.f;
+          mm = ok ? p.part_m[pr] : -INFINITY;
+          sa = ok ? p.part_scale[2 * pr] : 0.f;
+          sb = ok ? p.part_scale[2 * pr + 1] : 0.f;
         }
       }
-      const float wden = lane < nb ? exp2f(ls - mx) : 0.f;
-      wsum += wave_sum(wden);
-      float wlo = wden, whi = wden;
+      float wlo, whi;
       if constexpr (F16) {
-        const float a = lane < nb ? exp2f(mm - mx) : 0.f;
-        wlo = a * sa;
-        whi = a * sb;
+        const float a = exp2f(mm - mx) * inv;  // 0 for lanes past the task's slots
+        wlo = a * sa;  // columns 0..255 (lanes 0..31)
+        whi = a * sb;  // columns 256..511 (lanes 32..63)
+      } else {
+        wlo = whi = exp2f(ls - mx) * inv;
       }
       for (int j = 0; j < nb; j += 8) {
         if (i0 > 0 || j > 0) {
 #pragma unroll
           for (int u = 0; u < 8; ++u)
-            if (j + u < nb) d[u].load(src + (int64_t)(i0 + j + u) * sstride);
+            if (j + u < nb) d[k][u].load(src[k] + (int64_t)(g + G * (i0 + j + u)) * sstride);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           if (j + u < nb) {
-            // slot weights broadcast from lane j + u (wave-uniform index: v_readlane, no LDS)
             const float w0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wlo), j + u));
             const float w1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, whi), j + u));
-            d[u].fma(lane < 32 ? w0 : w1, o0, o1);
+            d[k][u].fma(lane < 32 ? w0 : w1, o[k][0], o[k][1]);
           }
         }
       }
     }
-    const float inv = 1.f / wsum;
-    o0 *= inv;
-    o1 *= inv;
   }
-  // o_merged in the projection's A-operand order: block (h, r / 32), k-step
-  // ks = lane / 2 (16 columns), lane slot (r % 32) + 32 (lane % 2): 8 floats.
-  float* dst = o_merged + (((int64_t)h * (Rp / 32) + r / 32) * (kDcP / 16) + (lane >> 1)) * 512 +
-               ((r & 31) + 32 * (lane & 1)) * 8;
-  *reinterpret_cast<f32x4*>(dst) = o0;
-  *reinterpret_cast<f32x4*>(dst + 4) = o1;
 }
 
-// project: one block per (weight head h, 32-row block rb, 32 output columns
-// dq), XCD-ordered so the 4 column blocks of (h, rb) share an L2. Wave w takes
-// the latent columns 128w .. 128w+127 (8 k-steps): A = merged O rows (fp32 in
-// the operand order the merge wrote, split into 16-bit hi/lo), B = 16
-// contiguous bytes of a W_UV row; the 4 partial 32x32 tiles are summed in LDS.
-// Every wave issues its 24 loads at once.
-template <typename WT>
-__global__ __launch_bounds__(256) void project_mfma_kernel(DecodeProblem p, const float* __restrict__ o_merged) {
-  typedef Mma<WT> M;
+// Merge + W_UV projection, one workgroup of 8 waves per (weight head h,
+// block of 16 query rows):
+//   1. each wave issues the loads of its W_UV operands (output columns
+//      16w .. 16w+15 of head h, all 512 latent columns: 16 x 16 B per lane),
+//      which stay in flight through the merge;
+//   2. the merge (merge_tasks): with 8 or more rows in the block, wave w
+//      merges rows w and w + 8, every slot; with fewer rows, each row's slots
+//      are split over G = 8 / rows waves (slot group w % G of row w / G) and
+//      the groups' sums added in LDS;
+//   3. out[row][16w + n] = sum_c O[row][c] W_UV[h dv + 16w + n][c] on
+//      v_mfma_f32_16x16x32 with A = O split into 16-bit high and low parts
+//      (two MFMAs, ~16 bits of the fp32 O) and B = the W_UV rows.
+// Blocks of one head run on one XCD (the dispatcher assigns id % 8 to XCDs),
+// so its 128 KB of W_UV is fetched once per head.
+constexpr int kMPWaves = 8;
+constexpr int kMPPitch = kDcP + 4;  // floats per LDS row of O
+
+template <typename WT, bool F16>
+__global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProblem p) {
+  typedef Mma16<WT> M;
   typedef typename M::vec vec;
-  __shared__ __attribute__((aligned(16))) float red[3][16][64];  // partial tiles of waves 1..3
+  constexpr float kLoScale = Mma<WT>::kLoScale;
+  __shared__ __attribute__((aligned(16))) float ot[kMPRows * kMPPitch];         // merged O rows
+  __shared__ __attribute__((aligned(16))) float gp[kMPWaves * kMPPitch];        // slot-group sums
   const int R = p.num_seqs * p.qps;
-  const int nrb = (R + 31) / 32;
+  const int nrb = (R + kMPRows - 1) / kMPRows;
   const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
-  const int grp = x + 8 * (k >> 2);  // (h, rb)
-  const int dq = k & 3;
-  if (grp >= p.nh * nrb) return;
-  const int h = grp / nrb, rb = grp % nrb;
+  const int h = (k / nrb) * 8 + x, rb = k % nrb;
+  if (h >= p.nh) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int rows = min(kMPRows, R - rb * kMPRows);
 
-  const float* oa = o_merged + (((int64_t)h * nrb + rb) * (kDcP / 16) + 8 * wave) * 512 + 8 * lane;
-  f32x4 olo[8], ohi[8];
+  // W_UV operands: B[k = 32 ks + 8 (lane / 16) + j][n = lane % 16]
+  //              = W_UV[h dv + 16 wave + lane % 16][32 ks + 8 (lane / 16) + j]
+  const WT* wrow = reinterpret_cast<const WT*>(p.W_UV) + ((int64_t)h * p.dv + 16 * wave + (lane & 15)) * kDcP +
+                   8 * (lane >> 4);
+  vec bw[16];
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {
-    olo[ks] = *reinterpret_cast<const f32x4*>(oa + 512 * ks);
-    ohi[ks] = *reinterpret_cast<const f32x4*>(oa + 512 * ks + 4);
+  for (int ks = 0; ks < 16; ++ks) bw[ks] = __builtin_bit_cast(vec, *reinterpret_cast<const i16x8*>(wrow + 32 * ks));
+
+  f32x4 o[2][2];
+  if (rows >= kMPWaves) {
+    const int t[2] = {rb * kMPRows + wave, wave + kMPWaves < rows ? rb * kMPRows + wave + kMPWaves : -1};
+    merge_tasks<F16>(p, t, h, 0, 1, lane, o);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int r = wave + kMPWaves * q;
+      if (r < kMPRows) {
+        *reinterpret_cast<f32x4*>(&ot[r * kMPPitch + 8 * lane]) = q == 0 || t[1] >= 0 ? o[q][0] : f32x4{};
+        *reinterpret_cast<f32x4*>(&ot[r * kMPPitch + 8 * lane + 4]) = q == 0 || t[1] >= 0 ? o[q][1] : f32x4{};
+      }
+    }
+    __syncthreads();
+  } else {
+    const int G = kMPWaves / rows;
+    const int r = wave / G, g = wave % G;
+    const int t[2] = {r < rows ? rb * kMPRows + r : -1, -1};
+    merge_tasks<F16>(p, t, h, g, G, lane, o);
+    *reinterpret_cast<f32x4*>(&gp[wave * kMPPitch + 8 * lane]) = o[0][0];
+    *reinterpret_cast<f32x4*>(&gp[wave * kMPPitch + 8 * lane + 4]) = o[0][1];
+    __syncthreads();
+    // O row r = sum of the G group rows of waves r G .. r G + G - 1; the
+    // block's other rows are zero
+    for (int i = tid; i < kMPRows * (kDcP / 4); i += kMPWaves * 64) {
+      const int rr = i / (kDcP / 4), c4 = i % (kDcP / 4);
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (rr < rows)
+        for (int q = 0; q < G; ++q) v += *reinterpret_cast<const f32x4*>(&gp[(rr * G + q) * kMPPitch + 4 * c4]);
+      *reinterpret_cast<f32x4*>(&ot[rr * kMPPitch + 4 * c4]) = v;
+    }
+    __syncthreads();
   }
-  const WT* wrow = reinterpret_cast<const WT*>(p.W_UV) + ((int64_t)h * p.dv + 32 * dq + (lane & 31)) * kDcP +
-                   128 * wave + 8 * (lane >> 5);
-  vec bw[8];
-#pragma unroll
-  for (int ks = 0; ks < 8; ++ks) bw[ks] = __builtin_bit_cast(vec, *reinterpret_cast<const i16x8*>(wrow + 16 * ks));
 
-  // out[row][32dq + n], partial over this wave's latent quarter
-  f32x16 acc_hi = {}, acc_lo = {};
+  // A[m = lane % 16][k = 32 ks + 8 (lane / 16) + j] = O[m][k]
+  f32x4 acc_hi = {}, acc_lo = {};
+  const float* arow = &ot[(lane & 15) * kMPPitch + 8 * (lane >> 4)];
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {
-    float o[8];
+  for (int ks = 0; ks < 16; ++ks) {
+    const f32x4 a0 = *reinterpret_cast<const f32x4*>(arow + 32 * ks);
+    const f32x4 a1 = *reinterpret_cast<const f32x4*>(arow + 32 * ks + 4);
+    float ov[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      o[e] = olo[ks][e];
-      o[4 + e] = ohi[ks][e];
+      ov[e] = a0[e];
+      ov[4 + e] = a1[e];
     }
-    vec vh, vl;
-    split8<WT>(o, vh, vl);
-    acc_hi = M::mma(vh, bw[ks], acc_hi);
-    acc_lo = M::mma(vl, bw[ks], acc_lo);
+    vec hi, lo;
+    split8<WT>(ov, hi, lo);
+    acc_hi = M::mma(hi, bw[ks], acc_hi);
+    acc_lo = M::mma(lo, bw[ks], acc_lo);
   }
-  f32x16 part;
+  // D[m = 4 (lane / 16) + i][n = lane % 16]
 #pragma unroll
-  for (int i = 0; i < 16; ++i) part[i] = acc_hi[i] + acc_lo[i] * (1.f / M::kLoScale);
-  if (wave > 0) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) red[wave - 1][i][lane] = part[i];
-  }
-  __syncthreads();
-  if (wave == 0) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float v = part[i] + red[0][i][lane] + red[1][i][lane] + red[2][i][lane];
-      const int r = 32 * rb + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-      if (r < R) p.out[((int64_t)r * p.nh + h) * p.dv + 32 * dq + (lane & 31)] = v;
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * (lane >> 4) + i;
+    if (r < rows) {
+      const int t = rb * kMPRows + r;
+      const int64_t orow = (int64_t)(t / p.qps) * p.Hq + (t % p.qps) * p.nh + h;
+      p.out[orow * p.dv + 16 * wave + (lane & 15)] = acc_hi[i] + acc_lo[i] * (1.f / kLoScale);
     }
   }
 }
@@ -477,35 +553,34 @@ hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype
 }
 
 bool project_mfma_supported(const DecodeProblem& p) {
-  return (p.wuv_dtype == LA_DTYPE_BF16 || p.wuv_dtype == LA_DTYPE_F16) && p.dc == kDcP && p.dv % 128 == 0 &&
-         p.dv == 128 && (reinterpret_cast<uintptr_t>(p.W_UV) & 15) == 0;
-}
-
-template <typename WT>
-hipError_t launch_proj(const DecodeProblem& p, const float* o_merged, hipStream_t stream) {
-  const int64_t groups = (int64_t)p.nh * ((p.num_seqs * p.qps + 31) / 32);  // (h, rb)
-  dim3 grid((unsigned)(8 * 4 * ((groups + 7) / 8)));
-  hipLaunchKernelGGL(project_mfma_kernel<WT>, grid, dim3(256), 0, stream, p, o_merged);
-  return hipGetLastError();
+  return (p.wuv_dtype == LA_DTYPE_BF16 || p.wuv_dtype == LA_DTYPE_F16) && p.dc == kDcP && p.dv == 128 &&
+         (reinterpret_cast<uintptr_t>(p.W_UV) & 15) == 0;
 }
 
 size_t combine_project_mfma_workspace(const DecodeProblem& p) {
-  const size_t rows = ((size_t)p.num_seqs * p.qps + 31) / 32 * 32;
-  return rows * p.nh * kDcP * sizeof(float);
+  (void)p;
+  return 0;  // the merged rows stay in LDS
 }
 
 hipError_t launch_combine_project_mfma(const DecodeProblem& p, float* o_merged, hipStream_t stream) {
-  const int64_t pairs = (int64_t)((p.num_seqs * p.qps + 31) / 32 * 32) * p.nh;  // rows padded to 32
-  if (p.num_seqs * p.qps == 0) return hipSuccess;
-  const dim3 grid((unsigned)((pairs + kMergeWaves - 1) / kMergeWaves));
-  if (p.part_f16)
-    hipLaunchKernelGGL((merge_slots_kernel<true>), grid, dim3(kMergeWaves * 64), 0, stream, p, o_merged);
-  else
-    hipLaunchKernelGGL((merge_slots_kernel<false>), grid, dim3(kMergeWaves * 64), 0, stream, p, o_merged);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (p.wuv_dtype == LA_DTYPE_BF16) return launch_proj<__hip_bfloat16>(p, o_merged, stream);
-  return launch_proj<__half>(p, o_merged, stream);
+  (void)o_merged;
+  const int R = p.num_seqs * p.qps;
+  if (R == 0) return hipSuccess;
+  const int nrb = (R + kMPRows - 1) / kMPRows;
+  // id = 8 (head / 8 * nrb + row block) + head % 8
+  const dim3 grid((unsigned)(8 * ((p.nh + 7) / 8) * nrb));
+  if (p.wuv_dtype == LA_DTYPE_BF16) {
+    if (p.part_f16)
+      hipLaunchKernelGGL((merge_project_kernel<__hip_bfloat16, true>), grid, dim3(kMPWaves * 64), 0, stream, p);
+    else
+      hipLaunchKernelGGL((merge_project_kernel<__hip_bfloat16, false>), grid, dim3(kMPWaves * 64), 0, stream, p);
+  } else {
+    if (p.part_f16)
+      hipLaunchKernelGGL((merge_project_kernel<__half, true>), grid, dim3(kMPWaves * 64), 0, stream, p);
+    else
+      hipLaunchKernelGGL((merge_project_kernel<__half, false>), grid, dim3(kMPWaves * 64), 0, stream, p);
+  }
+  return hipGetLastError();
 }
 
 }  // namespace la

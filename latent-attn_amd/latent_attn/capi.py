@@ -117,6 +117,8 @@ def load() -> ctypes.CDLL:
     lib.la_batched_fused_mla.argtypes = [vp, i32, i32, i32, vp, vp, vp, i32, vp, vp, vp, cfgp, vp, sz, vp]
     lib.la_fused_mla_workspace_size.restype = sz
     lib.la_fused_mla_workspace_size.argtypes = [i32, i32, cfgp]
+    lib.la_fused_mla_workspace_size_dt.restype = sz
+    lib.la_fused_mla_workspace_size_dt.argtypes = [i32, i32, cfgp, i32, i32]
     lib.la_absorb_q.restype = i32
     lib.la_absorb_q.argtypes = [vp, vp, i32, vp, i32, cfgp, vp]
     lib.la_naive_mla.restype = i32
