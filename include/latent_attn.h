@@ -227,6 +227,21 @@ size_t la_mla_decode_workspace_size(const la_decode_args* args);
  * combine -> W_UV projection. */
 int la_mla_decode(const la_decode_args* args, void* stream);
 
+/* la_mla_decode without any allocation. No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The scratch the
+ * step needs (16-bit queries, split partials) comes from a static device
+ * array of la_mla_decode_noalloc_max_bytes() bytes (64 MiB) that each GPU the
+ * library runs on holds until the process ends; args->workspace and
+ * workspace_bytes are ignored. Steps needing more than that return
+ * LA_ERROR_WORKSPACE before any device work (la_mla_decode_workspace_size
+ * gives the need). Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, two threads) race and must be serialised
+ * by the caller. Nothing in the array needs to start at zero; it keeps the
+ * last call's contents. */
+int la_mla_decode_noalloc(const la_decode_args* args, void* stream);
+size_t la_mla_decode_noalloc_max_bytes(void);
+
 /* Drop-in for launch_fused_mla (src/fused_mla.cuh:51): one query token over
  * one cache of seq_len rows. kv_cache / W_UV dtypes: F16 (the reference
  * contract), BF16 or F32. */

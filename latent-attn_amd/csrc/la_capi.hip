@@ -335,6 +335,40 @@ la_decode_args shared_cache_args(const void* kv_cache, int kv_dtype, int seq_len
   return a;
 }
 
+// Scratch of la_mla_decode_noalloc: one array per GPU, in the code object,
+// held until the process ends. Host code never uses the array's name as an
+// address (on the host it is only a stand-in for the device symbol): the
+// device address comes from hipGetSymbolAddress, once per device, with that
+// device current, and is kept per device.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+}  // namespace
+
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+// The current device's scratch address (looked up on its first use there).
+int scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return record_hip(e);
+  if (dev < 0 || dev >= kMaxDevices) return LA_ERROR_NOT_SUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return record_hip(e);
+    if (!ptr) return LA_ERROR_HIP;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return LA_SUCCESS;
+}
+
 }  // namespace
 }  // namespace la
 
@@ -363,6 +397,26 @@ size_t la_mla_decode_workspace_size(const la_decode_args* args) {
 }
 
 int la_mla_decode(const la_decode_args* args, void* stream) { return la::run(args, static_cast<hipStream_t>(stream)); }
+
+int la_mla_decode_noalloc(const la_decode_args* args, void* stream) {
+  la::DecodeProblem p;
+  la::Plan plan;
+  const int st = la::prepare(args, &p, &plan);
+  if (st != LA_SUCCESS) return st;
+  if (plan.total > la::kNoAllocScratchBytes) return LA_ERROR_WORKSPACE;
+  la_decode_args a = *args;
+  a.workspace = nullptr;
+  a.workspace_bytes = la::kNoAllocScratchBytes;
+  if (plan.total > 0) {
+    const int sp = la::scratch_ptr(&a.workspace);
+    if (sp != LA_SUCCESS) return sp;
+  } else {
+    a.workspace = &a;  // never dereferenced: the plan needs no workspace
+  }
+  return la::run(&a, static_cast<hipStream_t>(stream));
+}
+
+size_t la_mla_decode_noalloc_max_bytes(void) { return la::kNoAllocScratchBytes; }
 
 int la_fused_mla(const void* kv_cache, int kv_dtype, int seq_len, const float* q_absorbed, const float* q_rope,
                  const void* W_UV, int w_uv_dtype, const float* rope_cos, const float* rope_sin, float* output,

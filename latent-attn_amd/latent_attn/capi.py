@@ -111,6 +111,10 @@ def load() -> ctypes.CDLL:
     lib.la_mla_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs)]
     lib.la_mla_decode.restype = i32
     lib.la_mla_decode.argtypes = [ctypes.POINTER(DecodeArgs), vp]
+    lib.la_mla_decode_noalloc.restype = i32
+    lib.la_mla_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), vp]
+    lib.la_mla_decode_noalloc_max_bytes.restype = sz
+    lib.la_mla_decode_noalloc_max_bytes.argtypes = []
     lib.la_fused_mla.restype = i32
     lib.la_fused_mla.argtypes = [vp, i32, i32, vp, vp, vp, i32, vp, vp, vp, cfgp, vp, sz, vp]
     lib.la_batched_fused_mla.restype = i32
