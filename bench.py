@@ -251,10 +251,12 @@ def time_paged(lib, hip, capi, inp, out, ws, stream, bs: int = 64, steps: int = 
             "frac_of_8TBps": round(int(inp["total"]) * BYTES_PER_POS / (kern_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
-def time_fp8(lib, hip, capi, inp, out, stream, steps: int = 20) -> dict:
-    """The same decode step over an FP8 E4M3 copy of the cache (half the
-    bytes; staged as bf16 for the MFMA kernel): microseconds per step over `steps`
-    steps, and the latent-cache rate against 8 TB/s at 576 B per position."""
+def time_fp8(lib, hip, capi, inp, out, stream, steps: int = 100) -> dict:
+    """The same decode step over an FP8 E4M3 copy of the cache (576 B per
+    position, half the bytes; the MFMA kernel copies the fp8 rows and expands
+    them to bf16 in LDS): microseconds per step over `steps` steps, the
+    attention kernel's time (10 x 10 back-to-back launches), and the
+    latent-cache rates against 8 TB/s at 576 B per position."""
     import torch
 
     kv8 = inp["kv"].to(torch.float8_e4m3fn)
@@ -269,7 +271,7 @@ def time_fp8(lib, hip, capi, inp, out, stream, steps: int = 20) -> dict:
         if st != 0:
             raise RuntimeError(f"la_mla_decode (fp8): {lib.la_status_string(st).decode()}")
 
-    for _ in range(3):
+    for _ in range(20):
         step()
     t0, t1 = new_event(hip), new_event(hip)
     torch.cuda.synchronize()
@@ -281,8 +283,19 @@ def time_fp8(lib, hip, capi, inp, out, stream, steps: int = 20) -> dict:
     us = elapsed_ms(hip, t0, t1) * 1e3 / steps
     hip.hipEventDestroy(t0)
     hip.hipEventDestroy(t1)
-    return {"step_us": round(us, 1),
-            "cache_frac_of_8TBps": round(int(inp["total"]) * BYTES_PER_POS / 2 / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+    def step_ev(ev_b=None, ev_e=None, repeat=0):
+        a.decode_event_begin, a.decode_event_end, a.decode_repeat = ev_b, ev_e, repeat
+        step()
+
+    kern = time_attention(hip, step_ev)
+    kern_us = sum(kern) / len(kern) * 1e3
+    a.decode_event_begin = a.decode_event_end = None
+    a.decode_repeat = 0
+    fp8_bytes = int(inp["total"]) * BYTES_PER_POS // 2
+    return {"step_us": round(us, 2), "attn_kernel_us": round(kern_us, 2),
+            "cache_frac_of_8TBps": round(fp8_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+            "attn_frac_of_8TBps": round(fp8_bytes / (kern_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
 def time_layer(hip, inp, stream, calls: int = 20) -> dict:
@@ -547,8 +560,8 @@ def main():
                     help="comma-separated other configurations timed after the headline one ('' for none)")
     ap.add_argument("--no-mall-cold", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--fp8", action="store_true",
-                    help="also time the step over an FP8 E4M3 copy of the cache")
+    ap.add_argument("--no-fp8", action="store_true",
+                    help="skip the leg over an FP8 E4M3 copy of the cache")
     ap.add_argument("--layer", action="store_true",
                     help="also time LatentAttentionLayer.forward_batch (fp32 projections, 1.8 GB of weights) "
                          "on the same batch and cache")
@@ -604,7 +617,7 @@ def main():
     append_us = time_append(lib, hip, capi, inp, stream)
     paged = time_paged(lib, hip, capi, inp, step.out, step.ws, stream) if inp["offsets"] is None else None
     layer = time_layer(hip, inp, stream) if args.layer else None
-    fp8 = time_fp8(lib, hip, capi, inp, step.out, stream) if args.fp8 else None
+    fp8 = time_fp8(lib, hip, capi, inp, step.out, stream) if not args.no_fp8 and inp["offsets"] is None else None
     mall = None
     if not args.no_mall_cold:
         log("[bench] MALL-cold leg")

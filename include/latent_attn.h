@@ -70,9 +70,10 @@ typedef enum la_dtype {
   LA_DTYPE_BF16 = 2,
   /* OCP FP8 E4M3 ("e4m3fn": bias 7, no infinities, 0x7F / 0xFF NaN, max
    * 448), latent caches only (kv_dtype of decode, append and naive; not
-   * weights). Decode copies the rows to bf16 in the workspace (exact) for
-   * the MFMA kernel; kernel_variant 1 reads them on the VALU kernel. Values
-   * written by la_append_kv round to nearest even and saturate at +-448. */
+   * weights). The MFMA decode kernel reads the 576-B rows and expands each
+   * tile to bf16 in LDS (exact); kernel_variant 1 reads them on the VALU
+   * kernel. Values written by la_append_kv round to nearest even and
+   * saturate at +-448. */
   LA_DTYPE_FP8_E4M3 = 3
 } la_dtype;
 

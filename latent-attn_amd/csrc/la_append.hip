@@ -132,38 +132,4 @@ hipError_t launch_append(const AppendProblem& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-namespace {
-// FP8 E4M3 -> bf16, 16 values per thread per step. Every E4M3 value has at
-// most 4 significant bits and an exponent in [-9, 8], so it is a bf16 value
-// and its bf16 bits are the top half of its f32 bits (NaN codes give a bf16
-// NaN). Byte j of a 16-byte chunk is element j.
-__global__ __launch_bounds__(256) void fp8_to_bf16_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
-                                                          int64_t n16) {
-  for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256) {
-    const uint4 v = src[i];
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    uint32_t o[8];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint32_t lo = __float_as_uint(fp8_to_f32((w[k] >> (16 * h)) & 0xFFu)) >> 16;
-        const uint32_t hi = __float_as_uint(fp8_to_f32((w[k] >> (16 * h + 8)) & 0xFFu)) >> 16;
-        o[2 * k + h] = lo | (hi << 16);
-      }
-    dst[2 * i] = make_uint4(o[0], o[1], o[2], o[3]);
-    dst[2 * i + 1] = make_uint4(o[4], o[5], o[6], o[7]);
-  }
-}
-}  // namespace
-
-hipError_t launch_fp8_to_bf16(const void* src, void* dst, int64_t elems, hipStream_t stream) {
-  const int64_t n16 = elems / 16;
-  if (n16 <= 0) return hipSuccess;
-  const int64_t blocks = std::min<int64_t>((n16 + 255) / 256, 8192);
-  hipLaunchKernelGGL(fp8_to_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
-                     static_cast<const uint4*>(src), static_cast<uint4*>(dst), n16);
-  return hipGetLastError();
-}
-
 }  // namespace la

@@ -61,9 +61,6 @@ struct Plan {
   size_t part_scale_off = 0;
   bool absorb_mfma = false;  // q_nope . W_UK on the MFMA kernel
   bool absorb_prep = false;  // ... writing the attention kernel's 16-bit Q rows directly
-  bool stage_fp8 = false;    // fp8 cache staged as bf16 for the MFMA kernel
-  size_t stage_off = 0;
-  int64_t stage_elems = 0;
   size_t q_abs_off = 0, q_prep_off = 0, part_o_off = 0, part_lse_off = 0, o_merged_off = 0, total = 0;
 };
 
@@ -137,18 +134,8 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   if (a->total_rows > 0 && !a->kv_cache) return LA_ERROR_INVALID_VALUE;
 
   Plan pl;
-  // An FP8 E4M3 cache goes to the MFMA kernel through a bf16 copy in the
-  // workspace (every E4M3 value is a bf16 value), row for row, so offsets,
-  // lengths and block tables address it unchanged. The VALU kernel
-  // (kernel_variant 1) reads the fp8 rows directly.
-  bool stage = false;
-  if (p->kv_dtype == LA_DTYPE_FP8_E4M3 && variant != kGeneric &&
-      (reinterpret_cast<uintptr_t>(a->kv_cache) & 15) == 0 && a->total_rows * p->row_elems % 16 == 0) {
-    DecodeProblem ps = *p;
-    ps.kv_dtype = LA_DTYPE_BF16;
-    stage = mfma_supported(ps);
-    if (stage) p->kv_dtype = LA_DTYPE_BF16;
-  }
+  // An FP8 E4M3 cache runs on the MFMA kernel too (its tiles are expanded to
+  // bf16 in LDS); the VALU kernel (kernel_variant 1) reads it as well.
   const bool mfma_ok = mfma_supported(*p);
   if (variant == kMfma && !mfma_ok) return LA_ERROR_NOT_SUPPORTED;
   if (variant == kGeneric || !mfma_ok) {
@@ -209,12 +196,6 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
     pl.o_merged_off = off;
     off += align_up(combine_project_mfma_workspace(*p));
   }
-  if (stage) {
-    pl.stage_fp8 = true;
-    pl.stage_off = off;
-    pl.stage_elems = a->total_rows * (int64_t)p->row_elems;
-    off += align_up((size_t)pl.stage_elems * 2);
-  }
   pl.total = off;
 
   p->chunk_len = pl.chunk_len;
@@ -254,19 +235,13 @@ int run(const la_decode_args* a, hipStream_t stream) {
 
   const la_mla_config& c = a->cfg;
   const int64_t tokens = (int64_t)a->num_seqs * a->queries_per_seq;
-  if (plan.stage_fp8) {
-    p.kv = ws + plan.stage_off;
-    if (plan.num_chunks > 0) {
-      hipError_t e = launch_fp8_to_bf16(a->kv_cache, ws + plan.stage_off, plan.stage_elems, stream);
-      if (e != hipSuccess) return finish(e);
-    }
-  }
   if (plan.mfma) p.q_prep = ws + plan.q_prep_off;
   if (a->q_nope) {
     hipError_t e = hipSuccess;
     if (plan.absorb_prep) {
       // absorbed, scaled 16-bit Q rows for the attention kernel in one pass
-      e = launch_absorb_mfma(a->q_nope, a->W_UK, a->w_uk_dtype, p.q_prep, p.kv_dtype == LA_DTYPE_BF16 ? 1 : 2,
+      // q_prep in the MFMAs' 16-bit type: fp16 for an fp16 cache, bf16 otherwise
+      e = launch_absorb_mfma(a->q_nope, a->W_UK, a->w_uk_dtype, p.q_prep, p.kv_dtype == LA_DTYPE_F16 ? 2 : 1,
                              a->q_rope, p.scale_log2, c.qk_rope_head_dim, (int)tokens, c.num_heads,
                              c.qk_nope_head_dim, c.kv_lora_rank, a->queries_per_seq, stream);
     } else {

@@ -68,7 +68,7 @@ struct DecodeProblem {
   int Hq;                 // query heads per sequence = qps * nh
   const float* q_abs;     // (num_seqs*Hq, dc) f32
   const float* q_rope;    // (num_seqs*Hq, dR) f32
-  void* q_prep;           // MFMA path: [q_abs | q_rope] * scale_log2 in the cache's 16-bit
+  void* q_prep;           // MFMA path: [q_abs | q_rope] * scale_log2 in the MFMAs' 16-bit
                           // type, operand-order layout (qprep_index), written by
                           // launch_prep_q or the absorb kernel
   const void* W_UV;
@@ -288,14 +288,13 @@ hipError_t launch_naive(NaiveProblem p, void* workspace, hipStream_t stream);
 
 // Device-side cache append + query RoPE.
 hipError_t launch_append(const AppendProblem& p, hipStream_t stream);
-// elems FP8 E4M3 values at src -> bf16 at dst (exact); elems % 16 == 0, both 16-byte aligned
-hipError_t launch_fp8_to_bf16(const void* src, void* dst, int64_t elems, hipStream_t stream);
 
 // VALU split-KV decode: any dtype, kv_lora_rank <= 1024, qk_rope_head_dim <= 256.
 hipError_t launch_decode_generic(const DecodeProblem& p, hipStream_t stream);
 bool generic_supported(const DecodeProblem& p);
 
-// MFMA split-KV decode for 16-bit caches with kv_lora_rank 512, qk_rope_head_dim 64.
+// MFMA split-KV decode for 16-bit and FP8 E4M3 caches with kv_lora_rank 512,
+// qk_rope_head_dim 64.
 // ev_begin / ev_end (optional) are recorded at the kernel's start and end.
 hipError_t launch_decode_mfma(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_begin = nullptr,
                               hipEvent_t ev_end = nullptr);

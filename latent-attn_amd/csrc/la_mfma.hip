@@ -1,5 +1,6 @@
 // MFMA split-KV MLA decode kernel for gfx950 (MI355X): 16-bit latent cache
-// (bf16 or fp16), kv_lora_rank 512, qk_rope_head_dim 64.
+// (bf16 or fp16) or FP8 E4M3 cache (copied as fp8, expanded to bf16 tiles in
+// LDS), kv_lora_rank 512, qk_rope_head_dim 64.
 //
 // Math (paths relative to the reference repo): for each query head h and
 // cached position pos
@@ -410,6 +411,31 @@ struct TrPair {
 };
 
 constexpr int kRowBytes = (kDc + kDr) * 2;  // 1152: one packed cache row
+// Bytes of one cache row in HBM: a 16-bit row, or an FP8 E4M3 row (576).
+template <bool kFp8>
+constexpr int cache_row_bytes() { return kFp8 ? kDc + kDr : kRowBytes; }
+// FP8 E4M3 cache: wave w's 8 rows of a tile (576 B each, contiguous in HBM)
+// are copied packed to fp8_stage_off(w) .. + 4608 of the tile's buffer, in
+// kFp8RowCopies copies of 1 KB (lanes 0..31 of the last one). That range lies
+// inside the bytes of the wave's own bf16 rows 8w..8w+7 and below the k_rope
+// rows, so once the wave has read its staged rows (RoPE reads the k_rope
+// parts, expand_rows the c_t parts) it expands them in place to the bf16 tile
+// layout without touching another wave's staging. Every E4M3 value is a bf16
+// value, so the expanded tile is exactly what a bf16 cache holding the same
+// values gives.
+__host__ __device__ constexpr int fp8_stage_off(int w) { return 8704 * w + 4096; }
+constexpr int kFp8RowCopies = 5;  // 8 x 576 B = 4.5 KB
+constexpr int dma_per_wave(bool fp8) { return fp8 ? kFp8RowCopies + 2 : kDmaPerWave; }
+static_assert(fp8_stage_off(0) >= 0 && fp8_stage_off(3) + 8 * (kDc + kDr) <= kRopeOff, "staging below k_rope");
+// Wave w's expanded rows 8w..8w+7 stay clear of the other waves' staging.
+constexpr bool fp8_staging_disjoint() {
+  for (int w = 0; w < kWaves; ++w) {
+    if (w > 0 && ct_row_off(8 * w) < fp8_stage_off(w - 1) + 8 * (kDc + kDr)) return false;
+    if (w + 1 < kWaves && ct_row_off(8 * w + 7) + 2 * kDc > fp8_stage_off(w + 1)) return false;
+  }
+  return true;
+}
+static_assert(fp8_staging_disjoint(), "fp8 staging of one wave overlaps another wave's rows");
 // Cache policy of the cache-row copies: non-temporal (the nt bit of the gfx9.4+
 // cache-policy field). Every row is read exactly once per call; streaming the
 // ~300 MB past the caches keeps the weights, queries and partial slots of the
@@ -452,16 +478,17 @@ __device__ inline void tile_block_entry_async(const DecodeProblem& p, const SegC
 // First byte of tile k's first row: contiguous cache (entry unused) or the
 // pool block given by its table entry (clamped into the pool; pool rows fit
 // in 32 bits, which the launcher checks).
-template <bool kPaged>
+template <bool kPaged, bool kFp8>
 __device__ inline const char* tile_base(const DecodeProblem& p, const SegCtx& sg, int k, int entry) {
+  constexpr int kRowB = cache_row_bytes<kFp8>();
   if constexpr (kPaged) {
     const uint32_t q = tile_seq_index(sg, k);
     const uint32_t in_block = q - tile_block_index(p, q) * p.tile_per_block;
     const int b = min(max(__builtin_amdgcn_readfirstlane(entry), 0), p.pool_last);
     const uint32_t row = (uint32_t)b * (uint32_t)p.block_size + in_block * kT;
-    return reinterpret_cast<const char*>(p.kv) + (uint64_t)row * kRowBytes;
+    return reinterpret_cast<const char*>(p.kv) + (uint64_t)row * kRowB;
   } else {
-    return sg.base + (int64_t)(tile_eff(sg, k) * kT) * kRowBytes;
+    return sg.base + (int64_t)(tile_eff(sg, k) * kT) * kRowB;
   }
 }
 
@@ -478,15 +505,17 @@ struct TileDma {
   uint32_t ct, rope;
   int dlast;  // last - tb, wave-uniform
 };
+template <bool kFp8>
 __device__ inline TileDma tile_dma(const SegCtx& sg, int k, const char* base, int wave, int lane) {
+  constexpr int kRowB = cache_row_bytes<kFp8>();
   const int tb = k * kT + 8 * wave;
   const int t0 = tile_eff(sg, k) * kT;
   const int rr = lane >> 3;
   TileDma d;
   d.base = base;
-  d.ct = (uint32_t)(tb - t0) * kRowBytes + 16 * lane;
+  d.ct = (uint32_t)(tb - t0) * kRowB + 16 * lane;
   d.dlast = sg.last - tb;
-  d.rope = (uint32_t)(min(tb + rr, sg.last) - t0) * kRowBytes + kDc * 2 + 16 * ((lane & 7) ^ fr(8 * wave + rr));
+  d.rope = kFp8 ? 0u : (uint32_t)(min(tb + rr, sg.last) - t0) * kRowB + kDc * 2 + 16 * ((lane & 7) ^ fr(8 * wave + rr));
   return d;
 }
 
@@ -517,11 +546,48 @@ __device__ inline void issue_copy(const DecodeProblem& p, const SegCtx& sg, int 
   }
 }
 
-// All kDmaPerWave copies of tile k (base: tile_base of tile k).
+// FP8 cache: wave w's copy J of tile k. J < kFp8RowCopies: 1 KB of the
+// wave's 8 packed rows (chunk q = 64J + lane of 288 16-B chunks, i.e. row
+// q / 36, bytes 16 (q % 36) of it) to its staging bytes; past the segment's
+// last row each lane re-reads that chunk of the last row instead (rows past it
+// are masked, and unfilled capacity is never read). J = kFp8RowCopies /
+// + 1: the cos / sin rows, as for a 16-bit cache.
+template <int J>
+__device__ inline void issue_copy_fp8(const DecodeProblem& p, const SegCtx& sg, int k, lchar* L, uint32_t buf,
+                                      int wave, int lane, const TileDma& d) {
+  if constexpr (J < kFp8RowCopies) {
+    uint32_t off;
+    if (d.dlast >= 7) {  // wave-uniform: all 8 rows inside the segment
+      off = d.ct + 1024 * J;
+    } else {
+      const int q = 64 * J + lane;
+      const int r = (q * 1821) >> 16;  // q / 36, exact for q < 320
+      off = d.ct - 16 * lane + (uint32_t)(min(r, d.dlast) * (kDc + kDr) + 16 * (q - 36 * r));
+    }
+    lds_void* dst = (lds_void*)(L + buf + fp8_stage_off(wave) + 1024 * J);
+    if constexpr (J == kFp8RowCopies - 1) {
+      if (lane < 32) __builtin_amdgcn_global_load_lds(d.base + off, dst, 16, 0, kStreamPolicy);
+    } else {
+      __builtin_amdgcn_global_load_lds(d.base + off, dst, 16, 0, kStreamPolicy);
+    }
+  } else {
+    issue_copy<J - kFp8RowCopies + 9>(p, sg, k, L, buf, wave, lane, d);
+  }
+}
+
+template <bool kFp8, int J>
+__device__ inline void issue_copy_any(const DecodeProblem& p, const SegCtx& sg, int k, lchar* L, uint32_t buf,
+                                      int wave, int lane, const TileDma& d) {
+  if constexpr (kFp8) issue_copy_fp8<J>(p, sg, k, L, buf, wave, lane, d);
+  else issue_copy<J>(p, sg, k, L, buf, wave, lane, d);
+}
+
+// All copies of tile k (base: tile_base of tile k).
+template <bool kFp8>
 __device__ inline void issue_tile_dma(const DecodeProblem& p, const SegCtx& sg, int k, const char* base, lchar* L,
                                       uint32_t buf, int wave, int lane) {
-  const TileDma d = tile_dma(sg, k, base, wave, lane);
-  static_for<kDmaPerWave>([&](auto j) { issue_copy<decltype(j)::value>(p, sg, k, L, buf, wave, lane, d); });
+  const TileDma d = tile_dma<kFp8>(sg, k, base, wave, lane);
+  static_for<dma_per_wave(kFp8)>([&](auto j) { issue_copy_any<kFp8, decltype(j)::value>(p, sg, k, L, buf, wave, lane, d); });
 }
 
 // Rotate-half RoPE of rows 8w..8w+7 of the tile at LDS offset buf, in place
@@ -530,11 +596,16 @@ __device__ inline void issue_tile_dma(const DecodeProblem& p, const SegCtx& sg, 
 // rot_issue starts the four LDS reads (inline asm; the caller waits for them
 // with lgkmcnt), rot_finish rotates and stores.
 struct RotIn {
-  i16x4 ka, kb;
+  i16x4 ka, kb;      // 16-bit cache: k[i .. i+3], k[i+32 .. i+35]
+  uint32_t k8a, k8b;  // FP8 cache: the same elements as 4 + 4 codes
   f32x4 c, s;
   uint32_t pa, pb;
 };
 
+// FP8 cache: ka / kb are the 4 + 4 fp8 codes of the staged row (in their low
+// 32 bits); the rotated values go to the bf16 k_rope rows as for a 16-bit
+// cache.
+template <bool kFp8 = false>
 __device__ inline RotIn rot_issue(const lchar* L, uint32_t buf, int wave, int lane) {
   const int rl = lane >> 3, u = lane & 7;
   const int row = 8 * wave + rl;
@@ -542,22 +613,47 @@ __device__ inline RotIn rot_issue(const lchar* L, uint32_t buf, int wave, int la
   RotIn r;
   r.pa = buf + kRopeOff + row * 128 + (((u >> 1) ^ f) << 4) + 8 * (u & 1);
   r.pb = buf + kRopeOff + row * 128 + (((4 + (u >> 1)) ^ f) << 4) + 8 * (u & 1);
-  r.ka = lds_rd64(L, r.pa);
-  r.kb = lds_rd64(L, r.pb);
+  if constexpr (kFp8) {
+    const uint32_t src = buf + fp8_stage_off(wave) + rl * (kDc + kDr) + kDc + 4 * u;
+    r.k8a = __builtin_bit_cast(uint32_t, lds_rd32(L, src));
+    r.k8b = __builtin_bit_cast(uint32_t, lds_rd32(L, src + kDr / 2));
+  } else {
+    r.ka = lds_rd64(L, r.pa);
+    r.kb = lds_rd64(L, r.pb);
+  }
   r.c = lds_rd128<f32x4>(L, kCosOff + row * 128 + 16 * u);
   r.s = lds_rd128<f32x4>(L, kSinOff + row * 128 + 16 * u);
   return r;
 }
 
-template <typename KT>
+// Element e (0..3) of ka / kb as f32.
+template <typename KT, bool kFp8>
+__device__ inline float rot_k(const RotIn& in, bool second, int e) {
+  typedef typename Ops<KT>::elem E;
+  if constexpr (kFp8) {
+    const uint32_t w = second ? in.k8b : in.k8a;
+    const auto v = (e & 2) ? __builtin_amdgcn_cvt_pk_f32_fp8(w, true) : __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+    return v[e & 1];
+  } else {
+    return (float)__builtin_bit_cast(E, (short)(second ? in.kb[e] : in.ka[e]));
+  }
+}
+
+template <typename KT, bool kFp8>
+__device__ inline void rot_wait(RotIn& in) {
+  if constexpr (kFp8) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(in.k8a), "+v"(in.k8b), "+v"(in.c), "+v"(in.s));
+  else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(in.ka), "+v"(in.kb), "+v"(in.c), "+v"(in.s));
+}
+
+template <typename KT, bool kFp8>
 __device__ inline void rot_finish(lchar* L, RotIn& in) {
   typedef typename Ops<KT>::elem E;
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(in.ka), "+v"(in.kb), "+v"(in.c), "+v"(in.s));
+  rot_wait<KT, kFp8>(in);
   i16x4 ra, rb;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const float k0 = (float)__builtin_bit_cast(E, (short)in.ka[e]);
-    const float k1 = (float)__builtin_bit_cast(E, (short)in.kb[e]);
+    const float k0 = rot_k<KT, kFp8>(in, false, e);
+    const float k1 = rot_k<KT, kFp8>(in, true, e);
     ra[e] = __builtin_bit_cast(short, (E)(k0 * in.c[e] - k1 * in.s[e]));
     rb[e] = __builtin_bit_cast(short, (E)(k0 * in.s[e] + k1 * in.c[e]));
   }
@@ -578,10 +674,47 @@ __device__ inline void rot_store(lchar* L, const RotIn& in, const float (&ra)[4]
   lds_st(L, in.pb, b);
 }
 
-template <typename KT>
+template <typename KT, bool kFp8>
 __device__ inline void rotate_rows(lchar* L, uint32_t buf, int wave, int lane) {
-  RotIn r = rot_issue(L, buf, wave, lane);
-  rot_finish<KT>(L, r);
+  RotIn r = rot_issue<kFp8>(L, buf, wave, lane);
+  rot_finish<KT, kFp8>(L, r);
+}
+
+// FP8 cache: expands this wave's 8 staged rows of the tile at buf to the
+// bf16 c_t rows 8w..8w+7 (lane: latent columns 8 lane .. 8 lane + 7). All
+// eight reads complete before the first write, and the rows' k_rope parts
+// must have been read already (RoPE). Row j of the wave starts at
+// ct_row_off(8w) + 1088 j + 16 (j >= 4): (8w + j) / 4 % 4 steps by one at
+// j = 4 for every w.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// ds_read_b64 with immediate offset OFF (inline asm; the caller waits).
+template <int OFF>
+__device__ inline u32x2 lds_rd64_at(uint32_t off) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  u32x2 r;
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(off), "n"(OFF));
+  return r;
+}
+__device__ inline void expand_rows(lchar* L, uint32_t buf, int wave, int lane) {
+  const uint32_t src = buf + fp8_stage_off(wave) + 8 * lane;
+  const uint32_t dst = buf + ct_row_off(8 * wave) + 16 * lane;
+  u32x2 x[8];
+  static_for<8>([&](auto j_c) {
+    constexpr int j = decltype(j_c)::value;
+    x[j] = lds_rd64_at<j * (kDc + kDr)>(src);
+  });
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]),
+               "+v"(x[6]), "+v"(x[7]));
+  static_for<8>([&](auto j_c) {
+    constexpr int j = decltype(j_c)::value;
+    u32x4 y;
+    y[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x[j][0], 1.f, false));
+    y[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x[j][0], 1.f, true));
+    y[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x[j][1], 1.f, false));
+    y[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x[j][1], 1.f, true));
+    lds_st(L, dst + 1088 * j + (j >= 4 ? 16 : 0), y);
+  });
 }
 
 // Block id -> (chunk, head group), XCD-aware. Workgroups are dispatched
@@ -599,8 +732,12 @@ __device__ inline void block_coords(int num_chunks, int groups, int* chunk, int*
   *chunk = x * per + k / groups;
 }
 
-template <typename KT, bool kPaged>
+// kFp8: FP8 E4M3 cache rows (KT = bf16: the tiles are expanded to bf16 in
+// LDS and the MFMAs run on bf16).
+template <typename KT, bool kPaged, bool kFp8>
 __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, int groups) {
+  static_assert(!kFp8 || std::is_same<KT, __hip_bfloat16>::value, "fp8 tiles expand to bf16");
+  constexpr int kDma = dma_per_wave(kFp8);
   typedef Ops<KT> O_;
   typedef typename O_::vec vec;
   typedef typename O_::elem E;
@@ -632,7 +769,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     }
     const int64_t seg_hi = min(hi, s_hi);
     SegCtx sg;
-    sg.base = reinterpret_cast<const char*>(p.kv) + (kPaged ? 0 : lo * kRowBytes);
+    sg.base = reinterpret_cast<const char*>(p.kv) + (kPaged ? 0 : lo * cache_row_bytes<kFp8>());
     sg.pos0 = lo - s_lo;
     sg.last = (int)(seg_hi - lo - 1);
     sg.seq = s;
@@ -647,17 +784,17 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     // iteration -1); iteration t loads the entry of tile t+3 into blk_cur once
     // its own copies have their base, for the next iteration
     int blk_cur = 0;
-    const char* base0 = tile_base<kPaged>(p, sg, 0, 0);
+    const char* base0 = tile_base<kPaged, kFp8>(p, sg, 0, 0);
     if constexpr (kPaged) {
       const int e0 = tile_block_entry(p, sg, 0);
       blk_cur = tile_block_entry(p, sg, 1);
-      base0 = tile_base<kPaged>(p, sg, 0, e0);
+      base0 = tile_base<kPaged, kFp8>(p, sg, 0, e0);
     }
 
     // tile 1 rides along iteration -1; a fresh lane index keeps the per-lane
     // addresses out of the registers (and spill slots) that live across the
     // prologue: a spill reload here would wait on vmcnt and so serialise the copies
-    issue_tile_dma(p, sg, 0, base0, L, 0, wave, lane_id());
+    issue_tile_dma<kFp8>(p, sg, 0, base0, L, 0, wave, lane_id());
 
     // Q^T as the B operand: lane holds Q[head][16kk + 8*g2 .. +8], pre-scaled.
     // q_prep is stored in operand order (qprep_index): the wave's 32 rows form
@@ -693,7 +830,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     }
 
     wait_vm<0>();
-    rotate_rows<KT>(L, 0, wave, lane_id());  // fresh lane index: no spilled addresses
+    rotate_rows<KT, kFp8>(L, 0, wave, lane_id());  // fresh lane index: no spilled addresses
+    if constexpr (kFp8) expand_rows(L, 0, wave, lane_id());
 
     // Software pipeline over tiles; iteration t (from -1):
     //   [apply the rescale of own-head O rows decided by softmax(t)]
@@ -770,8 +908,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // 32kk: a lane base plus the immediate 32kk. For the 128-B k_rope rows
       // the byte offset is 16((2(kk-32) + g2) ^ fr(arow)) = 32(kk-32) ^
       // 16(g2 ^ fr(arow)): a lane constant XOR an immediate. A operands are
-      // read kQkDepth k-steps ahead of their MFMA. After the last tile the
-      // phase runs on a valid buffer and its result is dropped.
+      // read kQkDepth k-steps ahead of their MFMA. The last iteration skips
+      // the phase (no tile t+1).
       const int arow = lane & 31;
       const uint32_t ct_x = nxt + ct_row_off(arow) + 16 * g2;
       const uint32_t rp_x = (nxt + kRopeOff + arow * 128) | (16 * (g2 ^ fr(arow)));
@@ -779,7 +917,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // paged: this iteration's copies use tile t+2's entry (loaded in the
       // previous iteration or the prologue); tile t+3's goes out now and is
       // waited for by the next iteration's vmcnt(0)
-      const TileDma dm = tile_dma(sg, t + 2, tile_base<kPaged>(p, sg, t + 2, blk_cur), wave, lane);
+      const TileDma dm = tile_dma<kFp8>(sg, t + 2, tile_base<kPaged, kFp8>(p, sg, t + 2, blk_cur), wave, lane);
       if constexpr (kPaged) tile_block_entry_async(p, sg, t + 3, blk_cur);
       auto a_rd = [&](auto kk_c) -> vec {
         constexpr int kk = decltype(kk_c)::value;
@@ -806,8 +944,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       };
 
       f32x16 s_next;
-      vec ar[kQkDepth];
       vec pp[2];  // partner's P(t), read at step kQrAt
+      if (t + 1 < ntiles) {
+      vec ar[kQkDepth];
       static_for<kQkDepth>([&](auto i) { ar[decltype(i)::value] = a_rd(i); });
       static_for<36>([&](auto kk_c) {
         constexpr int kk = decltype(kk_c)::value;
@@ -826,11 +965,23 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           O_::mma_v(s_next, a, qb[kk]);
         }
         if constexpr (kk + D < 36) a = a_rd(std::integral_constant<int, kk + D>());
-        if constexpr (kk % 3 == 2 && kk / 3 < kDmaPerWave)
-          issue_copy<dma_order(kk / 3)>(p, sg, t + 2, L, dbuf, wave, lane, dm);
+        if constexpr (kk % 3 == 2 && kk / 3 < kDma) {
+          if constexpr (kFp8) issue_copy_fp8<kk / 3>(p, sg, t + 2, L, dbuf, wave, lane, dm);
+          else issue_copy<dma_order(kk / 3)>(p, sg, t + 2, L, dbuf, wave, lane, dm);
+        }
         if constexpr (kk >= kTrAt && kk - kTrAt < kPvDepth) b_issue(tr[kk - kTrAt], std::integral_constant<int, kk - kTrAt>());
         __builtin_amdgcn_sched_barrier(0);
       });
+      } else {
+        // The last iteration has no tile t+1 to score: only the LDS reads
+        // that PV(t) waits for go out, in QK's order (partner P, then the
+        // first kPvDepth value-read pairs), so PV's static counts still hold.
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(pflag));
+        pp[0] = lds_rd128<vec>(L, pp_x);
+        pp[1] = lds_rd128<vec>(L, pp_x + 1024);
+        static_for<kPvDepth>([&](auto i) { b_issue(tr[decltype(i)::value], i); });
+        s_next = f32x16{};
+      }
 
       // ---- softmax(t+1) pieces, spread over the PV(t) steps ----
       // s_next lane = head, 16 positions 8(i/4) + 4*g2 + (i%4); lazy base-2
@@ -949,13 +1100,12 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         // slot r: widen pair e = 2r, 2r+1 (r < 2); products of pair r-1,
         // sums of pair r-2; the last slot stores
         constexpr int r = decltype(slot_c)::value - kRotSlot0;
-        if constexpr (r == 0)
-          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(rot.ka), "+v"(rot.kb), "+v"(rot.c), "+v"(rot.s));
+        if constexpr (r == 0) rot_wait<KT, kFp8>(rot);
         if constexpr (r >= 0 && r < 2) {
 #pragma unroll
           for (int e = 2 * r; e < 2 * r + 2; ++e) {
-            rot_k0[e] = (float)__builtin_bit_cast(E, (short)rot.ka[e]);
-            rot_k1[e] = (float)__builtin_bit_cast(E, (short)rot.kb[e]);
+            rot_k0[e] = rot_k<KT, kFp8>(rot, false, e);
+            rot_k1[e] = rot_k<KT, kFp8>(rot, true, e);
             asm volatile("" : "+v"(rot_k0[e]), "+v"(rot_k1[e]));
           }
         }
@@ -992,13 +1142,18 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         O_::mma_a(acc[8 + cb], bvec, pp[ks]);
         if constexpr (step + kPvDepth < kPvSteps) b_issue(bc, std::integral_constant<int, step + kPvDepth>());
         if constexpr (step == kRotStep) {
-          wait_vm<kDmaPerWave - 3>();  // this wave's k_rope / cos / sin copies of tile t+2 have landed
-          rot = rot_issue(L, dbuf, wave, lane);
+          // this wave's k_rope / cos / sin copies of tile t+2 have landed (an
+          // fp8 tile's k_rope parts come with every row copy)
+          if constexpr (kFp8) wait_vm<0>();
+          else wait_vm<kDmaPerWave - 3>();
+          rot = rot_issue<kFp8>(L, dbuf, wave, lane);
         }
         sm_piece(std::integral_constant<int, 2 * step + 1>());
         rot_piece(std::integral_constant<int, 2 * step + 1>());
         __builtin_amdgcn_sched_barrier(0);
       });
+      // FP8 cache: tile t+2's staged rows to bf16 (RoPE has read their k_rope parts)
+      if constexpr (kFp8) expand_rows(L, dbuf, wave, lane_id());
       // ---- publish P(t+1) and softmax(t+1)'s rescale for the partner ----
       {
         const int npar = (t + 1) & 1;
@@ -1133,11 +1288,11 @@ __global__ __launch_bounds__(256) void prep_q_kernel(const float* __restrict__ q
   *reinterpret_cast<vec*>(out + qprep_index(qrow, 8 * j)) = v;
 }
 
-template <typename KT, bool kPaged>
+template <typename KT, bool kPaged, bool kFp8 = false>
 hipError_t launch_t(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
   static bool attr_set = false;  // per instance; setting it twice is harmless
   if (!attr_set) {
-    const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<KT, kPaged>);
+    const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<KT, kPaged, kFp8>);
     hipFuncAttributes fa;
     hipError_t e = hipFuncGetAttributes(&fa, fn);
     if (e != hipSuccess) return e;
@@ -1150,10 +1305,10 @@ hipError_t launch_t(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_be
   const int64_t blocks = (int64_t)((p.num_chunks + 7) / 8) * 8 * groups;
   if (ev_begin || ev_end) {
     // the events time this kernel's execution alone (no dispatch gap)
-    hipExtLaunchKernelGGL((decode_mfma_kernel<KT, kPaged>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes,
+    hipExtLaunchKernelGGL((decode_mfma_kernel<KT, kPaged, kFp8>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes,
                           stream, ev_begin, ev_end, 0, p, groups);
   } else {
-    hipLaunchKernelGGL((decode_mfma_kernel<KT, kPaged>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, stream,
+    hipLaunchKernelGGL((decode_mfma_kernel<KT, kPaged, kFp8>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, stream,
                        p, groups);
   }
   return hipGetLastError();
@@ -1180,7 +1335,7 @@ int mfma_heads_per_group() { return kHG; }
 int mfma_max_chunk_rows() { return kMaxChunkRows; }
 
 bool mfma_supported(const DecodeProblem& p) {
-  if (p.kv_dtype != LA_DTYPE_BF16 && p.kv_dtype != LA_DTYPE_F16) return false;
+  if (p.kv_dtype != LA_DTYPE_BF16 && p.kv_dtype != LA_DTYPE_F16 && p.kv_dtype != LA_DTYPE_FP8_E4M3) return false;
   if (p.dc != kDc || p.dR != kDr || p.Hq % 16 != 0 || p.Hq <= 0) return false;
   if (p.rope_rows > (1 << 24) || (p.rope_rows == 0 && p.total_rows > (1 << 24))) return false;
   // paged: a 32-row tile must lie inside one block
@@ -1198,7 +1353,7 @@ hipError_t launch_prep_q(const DecodeProblem& p, hipStream_t stream) {
   const int64_t threads = rows * ((kDc + kDr) / 8);
   if (threads == 0) return hipSuccess;
   const unsigned blocks = (unsigned)((threads + 255) / 256);
-  if (p.kv_dtype == LA_DTYPE_BF16)
+  if (p.kv_dtype != LA_DTYPE_F16)  // bf16 and fp8 caches run bf16 MFMAs
     hipLaunchKernelGGL(prep_q_kernel<__hip_bfloat16>, dim3(blocks), dim3(256), 0, stream, p.q_abs, p.q_rope,
                        p.scale_log2, reinterpret_cast<Ops<__hip_bfloat16>::elem*>(p.q_prep), rows, p.Hq);
   else
@@ -1209,9 +1364,11 @@ hipError_t launch_prep_q(const DecodeProblem& p, hipStream_t stream) {
 
 hipError_t launch_decode_mfma(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
   if (p.block_table) {
+    if (p.kv_dtype == LA_DTYPE_FP8_E4M3) return launch_t<__hip_bfloat16, true, true>(p, stream, ev_begin, ev_end);
     if (p.kv_dtype == LA_DTYPE_BF16) return launch_t<__hip_bfloat16, true>(p, stream, ev_begin, ev_end);
     return launch_t<__half, true>(p, stream, ev_begin, ev_end);
   }
+  if (p.kv_dtype == LA_DTYPE_FP8_E4M3) return launch_t<__hip_bfloat16, false, true>(p, stream, ev_begin, ev_end);
   if (p.kv_dtype == LA_DTYPE_BF16) return launch_t<__hip_bfloat16, false>(p, stream, ev_begin, ev_end);
   return launch_t<__half, false>(p, stream, ev_begin, ev_end);
 }

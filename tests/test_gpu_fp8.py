@@ -3,10 +3,11 @@
 The cache values are exactly the fp8 codes' values (oracle fp8_e4m3_decode);
 the VALU decode kernel (kernel_variant 1) and the naive path compute in fp32
 from them and are held to the fp32 tolerance against the float64 oracle
-(tests/conftest.py:assert_close). The default decode stages the fp8 rows as
-bf16 (exactly: every E4M3 value is a bf16 value) for the MFMA kernel, so it
-is held to the bf16 tolerance, and must equal that kernel run on a bf16 copy
-of the cache bit for bit, contiguous and paged. Appends are byte work: the stored codes must equal the
+(tests/conftest.py:assert_close). The default decode runs the MFMA kernel,
+which copies the fp8 rows and expands each tile to bf16 in LDS (exactly:
+every E4M3 value is a bf16 value), so it is held to the bf16 tolerance, and
+must equal that kernel run on a bf16 copy of the cache bit for bit,
+contiguous and paged. Appends are byte work: the stored codes must equal the
 oracle's encoding (round to nearest even, saturating at +-448) exactly.
 """
 
@@ -59,10 +60,10 @@ def test_fp8_decode_matches_oracle(cuda, lens0, variant, tol):
 
 
 @pytest.mark.parametrize("paged", [False, True])
-def test_fp8_staged_decode_equals_bf16_mfma(cuda, paged):
-    """The default fp8 decode (bf16 staging + MFMA kernel) gives exactly what
-    the MFMA kernel gives on a bf16 copy of the cache: the staging is exact
-    and the rest of the path is the same."""
+def test_fp8_mfma_decode_equals_bf16_mfma(cuda, paged):
+    """The default fp8 decode (fp8 rows expanded to bf16 in LDS by the MFMA
+    kernel) gives exactly what the MFMA kernel gives on a bf16 copy of the
+    cache: the expansion is exact and the rest of the path is the same."""
     cfg = MLAConfig.deepseek_v2()
     B, cap, bs = 3, 512, 64
     kv = fp8_cache((B, cap, ROW), 111, cuda)
