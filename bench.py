@@ -201,8 +201,9 @@ def time_paged(lib, hip, capi, inp, out, ws, stream, bs: int = 64, steps: int = 
     """The same decode step over a paged copy of the cache: every sequence's
     rows in blocks of `bs` rows scattered over a pool by a fixed permutation,
     read through a block table with device lengths (la_decode_args.block_table).
-    Step time over `steps` steps and the attention kernel's time (10 x 10
-    back-to-back launches), as for the contiguous line."""
+    Step time over `steps` steps (after 20 untimed steps and a 50-ms clock
+    settle) and the attention kernel's time (10 x 10 back-to-back launches),
+    as for the contiguous line."""
     import numpy as np
     import torch
 
@@ -229,8 +230,9 @@ def time_paged(lib, hip, capi, inp, out, ws, stream, bs: int = 64, steps: int = 
         if st != 0:
             raise RuntimeError(f"la_mla_decode (paged): {lib.la_status_string(st).decode()}")
 
-    for _ in range(50):
+    for _ in range(20):
         step()
+    settle_clocks(step, 50)
     t0, t1 = new_event(hip), new_event(hip)
     torch.cuda.synchronize()
     hip.hipEventRecord(t0, ctypes.c_void_p(stream))
@@ -254,8 +256,8 @@ def time_paged(lib, hip, capi, inp, out, ws, stream, bs: int = 64, steps: int = 
 def time_fp8(lib, hip, capi, inp, out, stream, steps: int = 100) -> dict:
     """The same decode step over an FP8 E4M3 copy of the cache (576 B per
     position, half the bytes; the MFMA kernel copies the fp8 rows and expands
-    them to bf16 in LDS): microseconds per step over `steps` steps, the
-    attention kernel's time (10 x 10 back-to-back launches), and the
+    them to bf16 in LDS): microseconds per step over `steps` steps (after 20
+    untimed steps and a 50-ms clock settle), the attention kernel's time (10 x 10 back-to-back launches), and the
     latent-cache rates against 8 TB/s at 576 B per position."""
     import torch
 
@@ -273,6 +275,7 @@ def time_fp8(lib, hip, capi, inp, out, stream, steps: int = 100) -> dict:
 
     for _ in range(20):
         step()
+    settle_clocks(step, 50)
     t0, t1 = new_event(hip), new_event(hip)
     torch.cuda.synchronize()
     hip.hipEventRecord(t0, ctypes.c_void_p(stream))

@@ -61,7 +61,7 @@ struct Plan {
   size_t part_scale_off = 0;
   bool absorb_mfma = false;  // q_nope . W_UK on the MFMA kernel
   bool absorb_prep = false;  // ... writing the attention kernel's 16-bit Q rows directly
-  size_t q_abs_off = 0, q_prep_off = 0, part_o_off = 0, part_lse_off = 0, o_merged_off = 0, total = 0;
+  size_t q_abs_off = 0, q_prep_off = 0, part_o_off = 0, part_lse_off = 0, total = 0;
 };
 
 // Fills the problem (without workspace pointers) and the plan. The args'
@@ -155,6 +155,12 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
     int64_t target_blocks = pl.mfma ? ncu : 4LL * ncu;
     int64_t chunks = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, groups));
     L = (total + chunks - 1) / chunks;
+    // MFMA path: a chunk writes Hq partial rows of dc fp16 values; keep them
+    // below the chunk's cache bytes (16-bit rows of dc + dR), so short
+    // batches (B = 1) do not trade a cheaper attention launch for a merge
+    // that reads more than the cache (Hq = 128: at least 128 rows).
+    if (pl.mfma) L = std::max<int64_t>(L, ((int64_t)p->Hq * c.kv_lora_rank + c.kv_lora_rank + c.qk_rope_head_dim - 1) /
+                                            (c.kv_lora_rank + c.qk_rope_head_dim));
     L = (L + 63) / 64 * 64;
     L = std::max<int64_t>(L, 64);
   }
@@ -192,10 +198,6 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   pl.part_lse_off = off;
   off += align_up((size_t)pl.num_slots * p->Hq * sizeof(float));
   pl.proj_mfma = project_mfma_supported(*p);
-  if (pl.proj_mfma) {
-    pl.o_merged_off = off;
-    off += align_up(combine_project_mfma_workspace(*p));
-  }
   pl.total = off;
 
   p->chunk_len = pl.chunk_len;
@@ -279,9 +281,7 @@ int run(const la_decode_args* a, hipStream_t stream) {
     }
     if (e != hipSuccess) return finish(e);
   }
-  return finish(plan.proj_mfma
-                    ? launch_combine_project_mfma(p, reinterpret_cast<float*>(ws + plan.o_merged_off), stream)
-                    : launch_combine_project(p, stream));
+  return finish(plan.proj_mfma ? launch_combine_project_mfma(p, stream) : launch_combine_project(p, stream));
 }
 
 la_decode_args shared_cache_args(const void* kv_cache, int kv_dtype, int seq_len, int batch, const float* q_absorbed,

@@ -317,10 +317,9 @@ hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype
                               const float* q_rope, float scale, int dR, int tokens, int nh, int dn, int dc, int qps,
                               hipStream_t stream);
 bool project_mfma_supported(const DecodeProblem& p);
-// Workspace bytes for the merged O (fp32, (num_seqs*Hq, dc)) the MFMA
-// combine + projection pair uses.
-size_t combine_project_mfma_workspace(const DecodeProblem& p);
-hipError_t launch_combine_project_mfma(const DecodeProblem& p, float* o_merged, hipStream_t stream);
+// Merge of the split partials and W_UV projection in one kernel (the merged
+// rows stay in LDS: no workspace).
+hipError_t launch_combine_project_mfma(const DecodeProblem& p, hipStream_t stream);
 
 // q_abs = q_nope . W_UK per head.
 hipError_t launch_absorb(const float* q_nope, const void* W_UK, int w_dtype, float* q_abs, int tokens, int nh, int dn,

@@ -7,22 +7,21 @@
 //             log-sum-exp merge of the split-KV partial slots
 //             (reference src/fused_mla.cu:255-267: normalise, then W_UV)
 //
-// Both run v_mfma_f32_32x32x16 with 32 query tokens as M. The fp32 operand
-// (q_nope, or the merged O) is split into a 16-bit high part and a 16-bit
-// residual (hi = rn(x), lo = rn(x - hi)); two MFMAs accumulate W*hi + W*lo in
-// fp32, so the result keeps ~16 bits of the fp32 operand instead of 8 (bf16)
-// or 11 (fp16). For fp16 the residual is pre-multiplied by 2^11 (and its
-// product by 2^-11) so it stays in the normal range.
+// absorb runs v_mfma_f32_32x32x16 with 32 query tokens as M, the projection
+// v_mfma_f32_16x16x32 with 16 query rows as M. The fp32 operand (q_nope, or
+// the merged O) is split into a 16-bit high part and a 16-bit residual
+// (hi = rn(x), lo = rn(x - hi)); two MFMAs accumulate W*hi + W*lo in fp32, so
+// the result keeps ~16 bits of the fp32 operand instead of 8 (bf16) or 11
+// (fp16). For fp16 the residual is pre-multiplied by 2^11 (and its product by
+// 2^-11) so it stays in the normal range.
 //
-// absorb:  grid (nh, dc/128, ceil(T/32)), 256 threads. W_UK[h][:, 128-col
-//          block] (128 x 128) is staged in LDS; wave w owns 32 columns; the
-//          B operand (8 consecutive rows i per lane) comes from
-//          ds_read_b64_tr_b16.
-// combine: merge_slots_kernel, one wave per (query row, weight head), writes
-//          the log-sum-exp merge of the partial slots (fp32, workspace, in the
-//          projection's A-operand order).
-// project: one block per (head, 32-row block, 32 output columns); the 4
-//          waves split the latent dimension and sum their tiles in LDS.
+// absorb:  one block of 256 threads per (32-token block, head, 128-column
+//          block), XCD-ordered; W_UK[h][:, 128-col block] (128 x 128) is
+//          staged in LDS; wave w owns 32 columns; the B operand (8
+//          consecutive rows i per lane) comes from ds_read_b64_tr_b16.
+// merge + project: merge_project_kernel, one block of 8 waves per (weight
+//          head, 16 query rows): the log-sum-exp merge of the partial slots
+//          into LDS, then the W_UV projection of the merged rows.
 #include "la_internal.hpp"
 
 #include <type_traits>
@@ -98,16 +97,17 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
   __shared__ __attribute__((aligned(16))) char wt[128 * kAbsRowBytes];  // dn <= 128 rows
   // q operands (hi, lo) of the 8 k-steps, shared by the 4 waves: [ks][hi|lo][lane] 16 B
   __shared__ __attribute__((aligned(16))) char qs[8 * 2 * 64 * 16];
-  // Block id -> (token block tb, head h, column block cb). The q_prep line of
-  // (token, 32-head group, k-step) gathers one 16-B slot from each head of the
-  // group, so the blocks of one (tb, head group, cb) run on one XCD (blocks go
-  // to XCDs round-robin by id % 8) and their slots meet in that XCD's L2
-  // instead of leaving it as partial lines.
-  const int ncb = dc / kAbsCols, nhg = (nh + 31) / 32;
+  // Block id -> (token block tb, head h, column block cb). A 128-B q_prep
+  // line gathers the 16-B slots of 8 consecutive heads (same token and
+  // k-step), and the ncb column blocks of a head read the same q_nope rows,
+  // so all blocks of one (tb, 8-head group) run on one XCD (blocks go to XCDs
+  // round-robin by id % 8): their slots meet in that XCD's L2 instead of
+  // leaving it as partial lines, and q_nope is fetched once per head.
+  const int ncb = dc / kAbsCols, nh8 = (nh + 7) / 8, gb = 8 * ncb;
   const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
-  const int grp = x + 8 * (k >> 5);  // (tb, head group, cb) group
-  const int tb = grp / (nhg * ncb), rem = grp - tb * (nhg * ncb);
-  const int h = 32 * (rem / ncb) + (k & 31), cb = rem % ncb, t0 = tb * 32;
+  const int grp = x + 8 * (k / gb), j = k % gb;  // (tb, 8-head group) group, block j in it
+  const int tb = grp / nh8;
+  const int h = 8 * (grp - tb * nh8) + (j & 7), cb = j >> 3, t0 = tb * 32;
   if (t0 >= tokens || h >= nh) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int nks = NKS > 0 ? NKS : dn / 16;  // <= 8
@@ -536,9 +536,10 @@ hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype
                               const float* q_rope, float scale, int dR, int tokens, int nh, int dn, int dc, int qps,
                               hipStream_t stream) {
   if (out_mode != 0 && (dc + dR != kQPrepRow || qps <= 0)) return hipErrorInvalidValue;
-  // one block per (token block, head, column block), ordered for the XCDs
-  const int64_t groups = (int64_t)((tokens + 31) / 32) * ((nh + 31) / 32) * (dc / kAbsCols);
-  dim3 grid((unsigned)(8 * 32 * ((groups + 7) / 8)));
+  // one block per (token block, head, column block), ordered for the XCDs:
+  // groups of (token block, 8 heads) with 8 * (dc / 128) blocks each
+  const int64_t groups = (int64_t)((tokens + 31) / 32) * ((nh + 7) / 8);
+  dim3 grid((unsigned)(8 * 8 * (dc / kAbsCols) * ((groups + 7) / 8)));
   const bool d128 = dn == 128;
   if (w_dtype == LA_DTYPE_BF16) {
     auto k = d128 ? absorb_mfma_kernel<__hip_bfloat16, 8> : absorb_mfma_kernel<__hip_bfloat16, 0>;
@@ -557,13 +558,7 @@ bool project_mfma_supported(const DecodeProblem& p) {
          (reinterpret_cast<uintptr_t>(p.W_UV) & 15) == 0;
 }
 
-size_t combine_project_mfma_workspace(const DecodeProblem& p) {
-  (void)p;
-  return 0;  // the merged rows stay in LDS
-}
-
-hipError_t launch_combine_project_mfma(const DecodeProblem& p, float* o_merged, hipStream_t stream) {
-  (void)o_merged;
+hipError_t launch_combine_project_mfma(const DecodeProblem& p, hipStream_t stream) {
   const int R = p.num_seqs * p.qps;
   if (R == 0) return hipSuccess;
   const int nrb = (R + kMPRows - 1) / kMPRows;
