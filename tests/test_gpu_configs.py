@@ -109,6 +109,32 @@ def test_config2_single_sequence(cuda, abi):
     assert_close(out[0], naive, "bf16", "cfg2 vs naive decompress-then-attend")
 
 
+def test_config2_plan_keeps_partials_below_cache(cuda, abi):
+    """At B = 1 the MFMA split plan gives every chunk at least ceil(Hq*512/576)
+    rows (128 at Hq = 128), so the fp16 partial rows it writes (Hq x 1 KB per
+    chunk) stay below the chunk's cache bytes: the workspace (16-bit q_prep,
+    partials, their scales, maxima and log-sum-exps) is bounded by the cache
+    bytes plus q_prep plus 16 B per partial row. Cutting 8,192 rows into one
+    chunk per CU (64 rows each) would need about twice the cache bytes."""
+    lib, capi = abi
+    inp = bench.build_inputs("cfg2", cuda)
+    cfg = inp["cfg"]
+    out = torch.empty(1, cfg.num_heads, cfg.v_head_dim, device=cuda)
+    a = bench.decode_args(inp, out, capi)
+    ws = lib.la_mla_decode_workspace_size(ctypes.byref(a))
+    S, H = inp["seq_len"], cfg.num_heads
+    cache_bytes = S * (cfg.kv_lora_rank + cfg.qk_rope_head_dim) * 2
+    q_prep = 128 * 576 * 2
+    chunks_max = S // 128                      # the plan's shortest chunk
+    bound = q_prep + chunks_max * H * (cfg.kv_lora_rank * 2 + 16) + 4 * 256
+    print(f"[cfg2 plan] workspace {ws} B, bound {bound} B, cache {cache_bytes} B", flush=True)
+    assert 0 < ws <= bound
+    assert ws - q_prep <= cache_bytes
+    # the explicit 64-row override still works and needs the larger workspace
+    a.chunk_rows = 64
+    assert lib.la_mla_decode_workspace_size(ctypes.byref(a)) > cache_bytes
+
+
 def test_config3_batched_uniform(cuda, abi):
     lib, capi = abi
     inp = bench.build_inputs("cfg3", cuda)
