@@ -97,6 +97,13 @@ constexpr int kPvSteps = 16;           // PV operand steps: (ks, column block), 
 constexpr int kPvDepth = 4;            // value-read pairs in flight (2 reads per step, lgkmcnt <= 15)
 constexpr int kRotStep = 9;            // PV step after which the RoPE reads of tile t+2 are issued
 constexpr int kRotSlot0 = 26;          // PV slots kRotSlot0 .. +5 rotate and store them
+// FP8 cache: the expansion of tile t+2's staged rows to bf16 runs inside PV(t):
+// rows 0..3 of the wave are read at step kRotStep (after the RoPE reads),
+// everything is waited for at step kExpWaitStep, rows 0..3 are converted and
+// stored in slots kExpSlot0 .. +3, rows 4..7 read after that and converted
+// and stored in slots kExpSlot0 + 4 .. +7.
+constexpr int kExpWaitStep = 12;
+constexpr int kExpSlot0 = 2 * kExpWaitStep;
 // Copy J of a tile goes out at QK step 3i + 2 for i with J = dma_order(i):
 // k_rope, cos and sin first, so the RoPE of the tile only waits for those.
 constexpr int dma_order(int i) { return (i + 8) % 11; }
@@ -144,6 +151,20 @@ constexpr int pv_later(int s) {
   }
   return -1;
 }
+// The lgkmcnt of PV step s's value-read wait. FP8 cache: the 4 expansion
+// reads of rows 0..3 go out with the RoPE reads at kRotStep (4 more later
+// operations for steps up to kExpWaitStep - 1); step kExpWaitStep waits for
+// everything issued so far (lgkmcnt 0), so the later steps' pairs are complete
+// and their waits only order the registers (15: never binding, at most 8 LDS
+// operations are outstanding then).
+constexpr int pv_wait_n(int s, bool fp8) {
+  if (!fp8 || s <= kRotStep) return pv_later(s);
+  if (s < kExpWaitStep) return pv_later(s) + 4 < 15 ? pv_later(s) + 4 : 15;
+  return s == kExpWaitStep ? 0 : 15;
+}
+static_assert(pv_wait_n(kExpWaitStep - 1, true) == pv_later(kExpWaitStep - 1) + 4, "fp8 expansion reads counted exactly");
+static_assert(kExpWaitStep > kRotStep && kExpWaitStep + 3 < kPvSteps && kExpSlot0 + 7 < 2 * kPvSteps,
+              "fp8 expansion slots inside PV");
 // Longest chunk the kernel accepts: keeps row byte offsets inside 32 bits.
 constexpr int kMaxChunkRows = 1 << 20;
 
@@ -717,6 +738,38 @@ __device__ inline void expand_rows(lchar* L, uint32_t buf, int wave, int lane) {
   });
 }
 
+// FP8 cache, the expansion spread over PV: the reads of staged rows
+// 4H .. 4H+3 of this wave (lane's 8 codes each) ...
+template <int H>
+__device__ inline void fp8_exp_issue(uint32_t src, u32x2 (&x)[4]) {
+  static_for<4>([&](auto i_c) {
+    constexpr int i = decltype(i_c)::value;
+    x[i] = lds_rd64_at<(4 * H + i) * (kDc + kDr)>(src);
+  });
+}
+// ... and row J's conversion and 16-B store (x read and waited for).
+template <int J>
+__device__ inline void fp8_exp_row(lchar* L, uint32_t dst, u32x2 x) {
+  u32x4 y;
+  y[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x[0], 1.f, false));
+  y[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x[0], 1.f, true));
+  y[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x[1], 1.f, false));
+  y[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x[1], 1.f, true));
+  lds_st(L, dst + 1088 * J + (J >= 4 ? 16 : 0), y);
+}
+// Rows 0..3's stores never reach staged rows 4..7 (every wave; rows 4..7's
+// stores reach staged rows 0..7, so all their reads complete first).
+constexpr bool fp8_half_order_ok() {
+  for (int w = 0; w < kWaves; ++w)
+    for (int j = 0; j < 4; ++j)
+      for (int i = 4; i < 8; ++i) {
+        const int a0 = ct_row_off(8 * w + j), s0 = fp8_stage_off(w) + i * (kDc + kDr);
+        if (a0 < s0 + kDc + kDr && s0 < a0 + 2 * kDc) return false;
+      }
+  return true;
+}
+static_assert(fp8_half_order_ok(), "fp8 expansion halves overlap");
+
 // Block id -> (chunk, head group), XCD-aware. Workgroups are dispatched
 // round-robin over the 8 XCDs (id % 8), each with its own L2. XCD x gets the
 // contiguous chunk range [x*per, (x+1)*per): the chunks of one sequence share
@@ -1094,13 +1147,29 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // landed; past the segment they rotate the clamped rows of a tile that
       // is never used). Softmax(t+1) and the rotation take two slots per step.
       operands_ready(p_cur[0], p_cur[1]);
+      u32x2 xe[4];  // FP8 cache: staged codes of half the wave's rows of tile t+2
+      const uint32_t e_src = dbuf + fp8_stage_off(wave) + 8 * lane;
+      const uint32_t e_dst = dbuf + ct_row_off(8 * wave) + 16 * lane;
+      auto exp_piece = [&](auto slot_c) {
+        constexpr int q = decltype(slot_c)::value - kExpSlot0;
+        if constexpr (kFp8 && q >= 0 && q < 8) {
+          if constexpr (q == 4)  // rows 4..7's reads (issued after slot 3) have landed
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xe[0]), "+v"(xe[1]), "+v"(xe[2]), "+v"(xe[3]));
+          fp8_exp_row<q>(L, e_dst, xe[q & 3]);
+          if constexpr (q == 3) fp8_exp_issue<1>(e_src, xe);
+        }
+      };
       RotIn rot;
       float rot_k0[4], rot_k1[4], rot_a[4], rot_b[4];
       auto rot_piece = [&](auto slot_c) {
         // slot r: widen pair e = 2r, 2r+1 (r < 2); products of pair r-1,
         // sums of pair r-2; the last slot stores
         constexpr int r = decltype(slot_c)::value - kRotSlot0;
-        if constexpr (r == 0) rot_wait<KT, kFp8>(rot);
+        if constexpr (r == 0) {
+          // FP8 cache: step kExpWaitStep has waited for the RoPE reads
+          if constexpr (kFp8) asm volatile("" : "+v"(rot.k8a), "+v"(rot.k8b), "+v"(rot.c), "+v"(rot.s));
+          else rot_wait<KT, kFp8>(rot);
+        }
         if constexpr (r >= 0 && r < 2) {
 #pragma unroll
           for (int e = 2 * r; e < 2 * r + 2; ++e) {
@@ -1121,8 +1190,16 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         constexpr int step = decltype(step_c)::value;
         constexpr int ks = step >> 3, cb = step & 7;
         TrPair& bc = tr[step % kPvDepth];
-        if constexpr (step == 0) wait_lgkm<pv_later(0)>(bc.x0, bc.x1, pp[0], pp[1]);
-        else wait_lgkm<pv_later(step)>(bc.x0, bc.x1);
+        if constexpr (step == 0) {
+          wait_lgkm<pv_later(0)>(bc.x0, bc.x1, pp[0], pp[1]);
+        } else if constexpr (kFp8 && step == kExpWaitStep) {
+          static_assert(pv_wait_n(kExpWaitStep, true) == 0, "full wait");
+          asm volatile("s_waitcnt lgkmcnt(0)"
+                       : "+v"(bc.x0), "+v"(bc.x1), "+v"(xe[0]), "+v"(xe[1]), "+v"(xe[2]), "+v"(xe[3]), "+v"(rot.k8a),
+                         "+v"(rot.k8b), "+v"(rot.c), "+v"(rot.s));
+        } else {
+          wait_lgkm<pv_wait_n(step, kFp8)>(bc.x0, bc.x1);
+        }
         i16x8 bv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -1138,6 +1215,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         __builtin_amdgcn_sched_barrier(0);
         sm_piece(std::integral_constant<int, 2 * step>());
         rot_piece(std::integral_constant<int, 2 * step>());
+        exp_piece(std::integral_constant<int, 2 * step>());
         __builtin_amdgcn_sched_barrier(0);
         O_::mma_a(acc[8 + cb], bvec, pp[ks]);
         if constexpr (step + kPvDepth < kPvSteps) b_issue(bc, std::integral_constant<int, step + kPvDepth>());
@@ -1147,13 +1225,13 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           if constexpr (kFp8) wait_vm<0>();
           else wait_vm<kDmaPerWave - 3>();
           rot = rot_issue<kFp8>(L, dbuf, wave, lane);
+          if constexpr (kFp8) fp8_exp_issue<0>(e_src, xe);
         }
         sm_piece(std::integral_constant<int, 2 * step + 1>());
         rot_piece(std::integral_constant<int, 2 * step + 1>());
+        exp_piece(std::integral_constant<int, 2 * step + 1>());
         __builtin_amdgcn_sched_barrier(0);
       });
-      // FP8 cache: tile t+2's staged rows to bf16 (RoPE has read their k_rope parts)
-      if constexpr (kFp8) expand_rows(L, dbuf, wave, lane_id());
       // ---- publish P(t+1) and softmax(t+1)'s rescale for the partner ----
       {
         const int npar = (t + 1) & 1;
