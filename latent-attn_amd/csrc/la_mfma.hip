@@ -276,6 +276,38 @@ __device__ inline void wait_vm() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | N);
 }
 
+// vmcnt(N) for N < 64 (gfx9 encoding: low 4 bits at [3:0], high 2 at
+// [15:14]), the other counters left alone.
+template <int N>
+__device__ inline void wait_vm_ext() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// QK step kk (a multiple of 6) of the first QK phase of a segment needs Q
+// k-steps kk .. kk+5, loaded by the prologue's 36 untracked loads after tile
+// 0's copies. Issued after Q k-step kk+5 by then: the 30 - kk later Q loads,
+// the tile copies of QK steps before kk (one at each step 3m + 2, m <
+// copies) and, paged, the table entry load before the phase. In every later
+// QK phase only those copies and that entry are outstanding, so the same
+// wait never binds there.
+template <int KK, int Copies, bool Paged>
+constexpr int qb_vm_n() {
+  int c = 0;
+  for (int m = 0; m < Copies; ++m)
+    if (3 * m + 2 < KK) ++c;
+  return (30 - KK) + c + (Paged ? 1 : 0);
+}
+template <int KK, int Copies, bool Paged, typename V>
+__device__ inline void qb_wait(V (&q)[36]) {
+  static_assert(KK % 6 == 0 && KK + 5 < 36, "six k-steps per wait");
+  constexpr int N = qb_vm_n<KK, Copies, Paged>();
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%6)"
+               : "+v"(q[KK]), "+v"(q[KK + 1]), "+v"(q[KK + 2]), "+v"(q[KK + 3]), "+v"(q[KK + 4]), "+v"(q[KK + 5])
+               : "n"(N));
+}
+
 // LDS-visibility barrier that leaves outstanding HBM->LDS copies in flight.
 // The "memory" clobber keeps the compiler from moving LDS accesses across it.
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
@@ -400,6 +432,33 @@ __device__ inline float dot2_e(__bf16 __attribute__((ext_vector_type(2))) p, flo
 __device__ inline float dot2_e(_Float16 __attribute__((ext_vector_type(2))) p, float c) {
   const _Float16 __attribute__((ext_vector_type(2))) one = {(_Float16)1.f, (_Float16)1.f};
   return __builtin_amdgcn_fdot2(p, one, c, false);
+}
+
+// The partner's rescale flag and the first six score operands of a QK phase,
+// in one asm statement that waits for the flag (issued first) before it
+// ends. A value read by one asm and waited for by a later one can be copied by
+// the compiler in between, before it has landed; the flag lives across the
+// whole phase, so it is complete where it is defined. The operands are waited
+// for by the phase's counted waits (the flag is not among their later reads).
+template <typename V>
+__device__ inline void qk_open(float& flag, V (&a)[6], uint32_t flag_at, uint32_t ct) {
+  asm volatile(
+      "ds_read_b32 %0, %7\n\t"
+      "ds_read_b128 %1, %8\n\t"
+      "ds_read_b128 %2, %8 offset:32\n\t"
+      "ds_read_b128 %3, %8 offset:64\n\t"
+      "ds_read_b128 %4, %8 offset:96\n\t"
+      "ds_read_b128 %5, %8 offset:128\n\t"
+      "ds_read_b128 %6, %8 offset:160\n\t"
+      "s_waitcnt lgkmcnt(6)"
+      : "=&v"(flag), "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3]), "=&v"(a[4]), "=&v"(a[5])
+      : "v"(flag_at), "v"(ct));
+}
+// The same flag alone, read and waited for in one asm statement.
+__device__ inline float lds_rd32_now(uint32_t off) {
+  float r;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(off));
+  return r;
 }
 
 // Marks v as produced here (no code): for a value read by inline asm whose
@@ -842,6 +901,10 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       const int e0 = tile_block_entry(p, sg, 0);
       blk_cur = tile_block_entry(p, sg, 1);
       base0 = tile_base<kPaged, kFp8>(p, sg, 0, e0);
+      // both entries have landed before the copies and the Q loads go out
+      // (the compiler's wait for blk_cur would otherwise count the untracked
+      // Q loads short and wait for most of them in the first QK phase)
+      asm volatile("" : "+v"(blk_cur));
     }
 
     // tile 1 rides along iteration -1; a fresh lane index keeps the per-lane
@@ -853,22 +916,23 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     // q_prep is stored in operand order (qprep_index): the wave's 32 rows form
     // one block and k-step kk is the coalesced 1 KB at element 512kk. All 36
     // k-steps (32 latent, 4 rope) stay in VGPRs for the segment. A wave
-    // without valid heads reads the group's last block (in bounds); lanes of
-    // invalid heads are zeroed.
+    // without valid heads reads the group's last block (in bounds); a lane of
+    // an invalid head reads the block's last valid row (finite values; its
+    // results are never stored, and it crosses the rescale threshold exactly
+    // when that row's head does).
+    // The 36 loads are inline asm, after tile 0's copies: the compiler does
+    // not track them, and the first QK phase waits for them k-step group by
+    // k-step group (qb_wait), so it overlaps the loads' tail.
     vec qb[36];
-    const bool q_head_ok = 32 * wave + (lane0 & 31) < hg_heads;
     {
       const int q_lane = lane_id();
       const int wblk = min(32 * wave, (hg_heads - 1) & ~31);
+      const int r = min(q_lane & 31, hg_heads - 1 - wblk);
       const int64_t qrow0 = (int64_t)s * qprep_rows_per_seq(p.Hq) + group * kHG + wblk;
       const E* qbase = reinterpret_cast<const E*>(p.q_prep) + qprep_index(qrow0, 0);
-      const vec* qsrc = reinterpret_cast<const vec*>(qbase) + q_lane;
+      const vec* qsrc = reinterpret_cast<const vec*>(qbase) + (r + (q_lane & 32));
 #pragma unroll
-      for (int kk = 0; kk < 36; ++kk) qb[kk] = qsrc[64 * kk];
-      const vec zero = {};
-#pragma unroll
-      for (int kk = 0; kk < 36; ++kk)
-        if (!q_head_ok) qb[kk] = zero;
+      for (int kk = 0; kk < 36; ++kk) asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(qb[kk]) : "v"(qsrc + 64 * kk));
     }
 
     float m_run = -INFINITY, l_run = 0.f;
@@ -882,7 +946,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       for (int nb = 0; nb < 16; ++nb) O_::mma_a0(acc[nb], z, z2);
     }
 
-    wait_vm<0>();
+    wait_vm_ext<36>();  // tile 0's copies have landed (the 36 Q loads went out after them)
     rotate_rows<KT, kFp8>(L, 0, wave, lane_id());  // fresh lane index: no spilled addresses
     if constexpr (kFp8) expand_rows(L, 0, wave, lane_id());
 
@@ -923,8 +987,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       }
     }
     for (int t = -1; t < ntiles; ++t) {
-      wait_vm<0>();   // this wave's copies of tile t+1 (issued in iteration t-1) have landed
-      if constexpr (kPaged) tie(blk_cur);  // and the table entry loaded with them
+      // this wave's copies of tile t+1 were waited for at the end of
+      // iteration t-1 (t = -1: tile 0 in the prologue; the Q loads are still
+      // in flight and QK(0) waits for them group by group)
       lds_barrier();  // tile t+1 staged and rotated by every wave; iteration t-1 done
       const int lane = lane_id();
       const int g2 = lane >> 5;
@@ -953,7 +1018,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         resc_pend = false;
       }
       // the partner's flag for the same rescale (applied to its rows before PV)
-      float pflag = lds_rd32(L, atab + pw * kAtabWave + 128);
+      // (read together with the first score operands of QK, qk_open)
+      const uint32_t pflag_at = atab + pw * kAtabWave + 128;
+      float pflag;
 
       // ---- QK(t+1): S^T[pos][head] over 36 k-steps (32 latent + 4 rope) ----
       // A operand of k-step kk: tile row arow = lane%32, logical chunk
@@ -1000,7 +1067,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       vec pp[2];  // partner's P(t), read at step kQrAt
       if (t + 1 < ntiles) {
       vec ar[kQkDepth];
-      static_for<kQkDepth>([&](auto i) { ar[decltype(i)::value] = a_rd(i); });
+      static_assert(kQkDepth == 6, "qk_open reads six operands");
+      qk_open(pflag, ar, pflag_at, ct_x);
       static_for<36>([&](auto kk_c) {
         constexpr int kk = decltype(kk_c)::value;
         constexpr int D = kQkDepth;
@@ -1010,7 +1078,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         }
         vec& a = ar[kk % D];
         wait_lgkm<qk_later(kk)>(a);
-        if constexpr (kk == 0) tie(pflag);  // issued before A(0), so complete
+        if constexpr (kk % 6 == 0) qb_wait<kk, kDma, kPaged>(qb);
         if constexpr (kk < 32) {
           if constexpr (kk == 0) O_::mma_v0(s_next, a, qb[kk]);
           else O_::mma_v(s_next, a, qb[kk]);
@@ -1029,7 +1097,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         // The last iteration has no tile t+1 to score: only the LDS reads
         // that PV(t) waits for go out, in QK's order (partner P, then the
         // first kPvDepth value-read pairs), so PV's static counts still hold.
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(pflag));
+        pflag = lds_rd32_now(pflag_at);
         pp[0] = lds_rd128<vec>(L, pp_x);
         pp[1] = lds_rd128<vec>(L, pp_x + 1024);
         static_for<kPvDepth>([&](auto i) { b_issue(tr[decltype(i)::value], i); });
@@ -1245,6 +1313,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         if (lane < 32) lds_st(L, natab + 4 * lane, alpha_pend);
         if (lane == 0) lds_st(L, natab + 128, resc_pend ? 1.f : 0.f);
       }
+      wait_vm<0>();  // this wave's copies of tile t+2 (issued in this iteration) have landed
+      if constexpr (kPaged) tie(blk_cur);  // and the table entry loaded with them
     }
 
     wait_vm<0>();  // the last iteration's copies (of a tile past the segment) have landed

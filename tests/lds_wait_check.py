@@ -1,0 +1,82 @@
+"""Static check of the attention kernel's LDS read waits in compiled gfx950
+assembly (test infrastructure).
+
+The MFMA decode kernel issues its LDS reads as inline asm and waits for them
+with counted ``s_waitcnt lgkmcnt(N)`` statements of its own, so the compiler
+does not know when a read's destination registers are written. If it copies
+or otherwise touches such a register between the read and the wait that
+retires it, that instruction sees stale data. This module walks a kernel's
+instructions in order with an in-order model of the LDS counter: every LDS
+operation is pending until a wait retires it (``lgkmcnt(N)`` retires all but
+the newest N), and any other instruction that reads or writes a register a
+pending read will write is reported.
+
+The walk is linear: branches are not followed, so code of a skipped arm is
+scanned in place. That over-approximates the pending set on some paths and
+is exact on the straight-line hot loop.
+"""
+
+from __future__ import annotations
+
+import re
+
+
+def _regs(tok: str) -> set:
+    tok = tok.strip()
+    m = re.match(r"([va])\[(\d+):(\d+)\]", tok)
+    if m:
+        return {(m.group(1), i) for i in range(int(m.group(2)), int(m.group(3)) + 1)}
+    m = re.match(r"([va])(\d+)\b", tok)
+    if m:
+        return {(m.group(1), int(m.group(2)))}
+    return set()
+
+
+def _operands(line: str) -> list:
+    parts = line.split(None, 1)
+    return re.split(r",\s*", parts[1]) if len(parts) > 1 else []
+
+
+def kernels(asm: str, prefix: str) -> dict:
+    """{symbol: [instruction lines]} for every function whose symbol starts
+    with ``prefix`` in an assembly listing."""
+    out, cur = {}, None
+    for line in asm.splitlines():
+        m = re.match(r"^(\S+):", line)
+        if m and m.group(1).startswith(prefix):
+            cur = m.group(1)
+            out[cur] = []
+            continue
+        if cur is None:
+            continue
+        if line.startswith(".Lfunc_end"):
+            cur = None
+            continue
+        s = line.strip()
+        if s and not s.startswith((";", ".")) and not re.match(r"^\.?L\w*:", s):
+            out[cur].append(s)
+    return out
+
+
+def pending_uses(instrs: list) -> list:
+    """Instructions that touch a register an unretired LDS read will write."""
+    pend = []  # (destination registers, index of the read)
+    bad = []
+    for n, ins in enumerate(instrs):
+        op = ins.split()[0]
+        if op == "s_waitcnt":
+            m = re.search(r"lgkmcnt\((\d+)\)", ins)
+            if m:
+                k = int(m.group(1))
+                pend = pend[len(pend) - k:] if 0 < k < len(pend) else ([] if k == 0 else pend)
+            continue
+        ops = _operands(ins)
+        used = set()
+        for o in ops[1:] if op.startswith("ds_read") else ops:
+            used |= _regs(o)
+        for dest, at in pend:
+            if dest & used:
+                bad.append((n, ins, at, instrs[at]))
+        if op.startswith("ds_"):
+            pend.append((_regs(ops[0]) if op.startswith("ds_read") else set(), n))
+    return bad
