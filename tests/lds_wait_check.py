@@ -9,7 +9,8 @@ retires it, that instruction sees stale data. This module walks a kernel's
 instructions in order with an in-order model of the LDS counter: every LDS
 operation is pending until a wait retires it (``lgkmcnt(N)`` retires all but
 the newest N), and any other instruction that reads or writes a register a
-pending read will write is reported.
+pending read will write is reported (vector-memory loads can be tracked the
+same way against vmcnt).
 
 The walk is linear: branches are not followed, so code of a skipped arm is
 scanned in place. That over-approximates the pending set on some paths and
@@ -58,25 +59,41 @@ def kernels(asm: str, prefix: str) -> dict:
     return out
 
 
-def pending_uses(instrs: list) -> list:
-    """Instructions that touch a register an unretired LDS read will write."""
-    pend = []  # (destination registers, index of the read)
+def _retire(pend: list, k: int) -> list:
+    return [] if k == 0 else (pend[len(pend) - k:] if k < len(pend) else pend)
+
+
+def pending_uses(instrs: list, counters=("lgkm",)) -> list:
+    """Instructions that touch a register an unretired LDS read (counter
+    "lgkm") or vector-memory load ("vm") will write. Vector-memory operations
+    are modelled like LDS operations with their own in-order counter (stores
+    and HBM->LDS copies count without a destination). The vm model also
+    reports reads the compiler makes of an unused register half (the high half
+    of a v_mad_u64_u32 addend whose result it truncates), which are harmless,
+    so the kernel test applies only the lgkm model."""
+    pend = {"lgkm": [], "vm": []}  # counter -> [(destination registers, index)]
     bad = []
     for n, ins in enumerate(instrs):
         op = ins.split()[0]
         if op == "s_waitcnt":
-            m = re.search(r"lgkmcnt\((\d+)\)", ins)
-            if m:
-                k = int(m.group(1))
-                pend = pend[len(pend) - k:] if 0 < k < len(pend) else ([] if k == 0 else pend)
+            for cnt in ("lgkm", "vm"):
+                m = re.search(cnt + r"cnt\((\d+)\)", ins)
+                if m:
+                    pend[cnt] = _retire(pend[cnt], int(m.group(1)))
             continue
         ops = _operands(ins)
+        is_load = op.startswith(("global_load", "buffer_load")) and "_lds_" not in op
+        vmem = op.startswith(("global_", "buffer_", "scratch_"))
+        reads_dest = op.startswith("ds_read") or is_load
         used = set()
-        for o in ops[1:] if op.startswith("ds_read") else ops:
+        for o in ops[1:] if reads_dest else ops:
             used |= _regs(o)
-        for dest, at in pend:
-            if dest & used:
-                bad.append((n, ins, at, instrs[at]))
+        for cnt in counters:
+            for dest, at in pend[cnt]:
+                if dest & used:
+                    bad.append((n, ins, at, instrs[at]))
         if op.startswith("ds_"):
-            pend.append((_regs(ops[0]) if op.startswith("ds_read") else set(), n))
+            pend["lgkm"].append((_regs(ops[0]) if op.startswith("ds_read") else set(), n))
+        elif vmem:
+            pend["vm"].append((_regs(ops[0]) if is_load else set(), n))
     return bad
