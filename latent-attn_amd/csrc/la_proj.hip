@@ -430,22 +430,29 @@ __device__ inline void merge_tasks(const DecodeProblem& p, const int (&t)[2], in
 //   2. the merge (merge_tasks): with 8 or more rows in the block, wave w
 //      merges rows w and w + 8, every slot; with fewer rows, each row's slots
 //      are split over G = 8 / rows waves (slot group w % G of row w / G) and
-//      the groups' sums added in LDS;
+//      the groups' sums added in LDS. Each merged fp32 element is split once
+//      into a 16-bit high part and a residual (split8), which go to LDS as
+//      the projection's A operands;
 //   3. out[row][16w + n] = sum_c O[row][c] W_UV[h dv + 16w + n][c] on
-//      v_mfma_f32_16x16x32 with A = O split into 16-bit high and low parts
-//      (two MFMAs, ~16 bits of the fp32 O) and B = the W_UV rows.
+//      v_mfma_f32_16x16x32: two MFMAs per k-step (A = the high and the low
+//      rows, ~16 bits of the fp32 O; B = the W_UV rows).
 // Blocks of one head run on one XCD (the dispatcher assigns id % 8 to XCDs),
 // so its 128 KB of W_UV is fetched once per head.
 constexpr int kMPWaves = 8;
-constexpr int kMPPitch = kDcP + 4;  // floats per LDS row of O
+constexpr int kMPPitch = kDcP + 4;  // floats per LDS row of a slot-group sum
+// 16-bit elements per LDS row of the high / low operand rows: 1040 B, 16 B
+// past a multiple of 256, so the 16 rows one A read touches (16 lanes, one
+// 16-B column each) fall on distinct banks
+constexpr int kMPOPitch = kDcP + 8;
 
 template <typename WT, bool F16>
 __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProblem p) {
   typedef Mma16<WT> M;
   typedef typename M::vec vec;
   constexpr float kLoScale = Mma<WT>::kLoScale;
-  __shared__ __attribute__((aligned(16))) float ot[kMPRows * kMPPitch];         // merged O rows
-  __shared__ __attribute__((aligned(16))) float gp[kMPWaves * kMPPitch];        // slot-group sums
+  __shared__ __attribute__((aligned(16))) short oh[kMPRows * kMPOPitch];      // merged O rows, high parts
+  __shared__ __attribute__((aligned(16))) short ol[kMPRows * kMPOPitch];      // and residuals
+  __shared__ __attribute__((aligned(16))) float gp[kMPWaves * kMPPitch];      // slot-group sums
   const int R = p.num_seqs * p.qps;
   const int nrb = (R + kMPRows - 1) / kMPRows;
   const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
@@ -462,17 +469,27 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
 #pragma unroll
   for (int ks = 0; ks < 16; ++ks) bw[ks] = __builtin_bit_cast(vec, *reinterpret_cast<const i16x8*>(wrow + 32 * ks));
 
+  // row r, columns c0 .. c0 + 7 of O -> high and low operand rows
+  auto put8 = [&](int r, int c0, const float (&v)[8]) {
+    vec hi, lo;
+    split8<WT>(v, hi, lo);
+    *reinterpret_cast<vec*>(&oh[r * kMPOPitch + c0]) = hi;
+    *reinterpret_cast<vec*>(&ol[r * kMPOPitch + c0]) = lo;
+  };
   f32x4 o[2][2];
   if (rows >= kMPWaves) {
     const int t[2] = {rb * kMPRows + wave, wave + kMPWaves < rows ? rb * kMPRows + wave + kMPWaves : -1};
     merge_tasks<F16>(p, t, h, 0, 1, lane, o);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int r = wave + kMPWaves * q;
-      if (r < kMPRows) {
-        *reinterpret_cast<f32x4*>(&ot[r * kMPPitch + 8 * lane]) = q == 0 || t[1] >= 0 ? o[q][0] : f32x4{};
-        *reinterpret_cast<f32x4*>(&ot[r * kMPPitch + 8 * lane + 4]) = q == 0 || t[1] >= 0 ? o[q][1] : f32x4{};
+      const bool live = q == 0 || t[1] >= 0;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = live ? o[q][0][e] : 0.f;
+        v[4 + e] = live ? o[q][1][e] : 0.f;
       }
+      put8(wave + kMPWaves * q, 8 * lane, v);
     }
     __syncthreads();
   } else {
@@ -485,31 +502,32 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
     __syncthreads();
     // O row r = sum of the G group rows of waves r G .. r G + G - 1; the
     // block's other rows are zero
-    for (int i = tid; i < kMPRows * (kDcP / 4); i += kMPWaves * 64) {
-      const int rr = i / (kDcP / 4), c4 = i % (kDcP / 4);
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    for (int i = tid; i < kMPRows * (kDcP / 8); i += kMPWaves * 64) {
+      const int rr = i / (kDcP / 8), c8 = i % (kDcP / 8);
+      f32x4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = v0;
       if (rr < rows)
-        for (int q = 0; q < G; ++q) v += *reinterpret_cast<const f32x4*>(&gp[(rr * G + q) * kMPPitch + 4 * c4]);
-      *reinterpret_cast<f32x4*>(&ot[rr * kMPPitch + 4 * c4]) = v;
+        for (int q = 0; q < G; ++q) {
+          v0 += *reinterpret_cast<const f32x4*>(&gp[(rr * G + q) * kMPPitch + 8 * c8]);
+          v1 += *reinterpret_cast<const f32x4*>(&gp[(rr * G + q) * kMPPitch + 8 * c8 + 4]);
+        }
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = v0[e];
+        v[4 + e] = v1[e];
+      }
+      put8(rr, 8 * c8, v);
     }
     __syncthreads();
   }
 
-  // A[m = lane % 16][k = 32 ks + 8 (lane / 16) + j] = O[m][k]
+  // A[m = lane % 16][k = 32 ks + 8 (lane / 16) + j] = O[m][k] (high, low)
   f32x4 acc_hi = {}, acc_lo = {};
-  const float* arow = &ot[(lane & 15) * kMPPitch + 8 * (lane >> 4)];
+  const int a0 = (lane & 15) * kMPOPitch + 8 * (lane >> 4);
 #pragma unroll
   for (int ks = 0; ks < 16; ++ks) {
-    const f32x4 a0 = *reinterpret_cast<const f32x4*>(arow + 32 * ks);
-    const f32x4 a1 = *reinterpret_cast<const f32x4*>(arow + 32 * ks + 4);
-    float ov[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      ov[e] = a0[e];
-      ov[4 + e] = a1[e];
-    }
-    vec hi, lo;
-    split8<WT>(ov, hi, lo);
+    const vec hi = *reinterpret_cast<const vec*>(&oh[a0 + 32 * ks]);
+    const vec lo = *reinterpret_cast<const vec*>(&ol[a0 + 32 * ks]);
     acc_hi = M::mma(hi, bw[ks], acc_hi);
     acc_lo = M::mma(lo, bw[ks], acc_lo);
   }
