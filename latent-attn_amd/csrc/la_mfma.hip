@@ -104,8 +104,11 @@ constexpr int kRotSlot0 = 26;          // PV slots kRotSlot0 .. +5 rotate and st
 // and stored in slots kExpSlot0 + 4 .. +7.
 constexpr int kExpWaitStep = 12;
 constexpr int kExpSlot0 = 2 * kExpWaitStep;
-// Copy J of a tile goes out at QK step 3i + 2 for i with J = dma_order(i):
-// k_rope, cos and sin first, so the RoPE of the tile only waits for those.
+// Copy J of a tile goes out at QK step copy_step(i) for i with J =
+// dma_order(i): k_rope, cos and sin first, so the RoPE of the tile only waits
+// for those.
+constexpr int kCopyFirst = 2, kCopyStride = 3;
+constexpr int copy_step(int i) { return kCopyFirst + kCopyStride * i; }
 constexpr int dma_order(int i) { return (i + 8) % 11; }
 constexpr int kQrAt = 32 - kQkDepth;   // QK step before which the partner-P reads are issued
 constexpr int kTrAt = 36 - kPvDepth;   // QK steps kTrAt.. issue the first kPvDepth PV value-read pairs
@@ -287,7 +290,7 @@ __device__ inline void wait_vm_ext() {
 // QK step kk (a multiple of 6) of the first QK phase of a segment needs Q
 // k-steps kk .. kk+5, loaded by the prologue's 36 untracked loads after tile
 // 0's copies. Issued after Q k-step kk+5 by then: the 30 - kk later Q loads,
-// the tile copies of QK steps before kk (one at each step 3m + 2, m <
+// the tile copies of QK steps before kk (copy m at step copy_step(m), m <
 // copies) and, paged, the table entry load before the phase. In every later
 // QK phase only those copies and that entry are outstanding, so the same
 // wait never binds there.
@@ -295,7 +298,7 @@ template <int KK, int Copies, bool Paged>
 constexpr int qb_vm_n() {
   int c = 0;
   for (int m = 0; m < Copies; ++m)
-    if (3 * m + 2 < KK) ++c;
+    if (copy_step(m) < KK) ++c;
   return (30 - KK) + c + (Paged ? 1 : 0);
 }
 template <int KK, int Copies, bool Paged, typename V>
@@ -1086,9 +1089,10 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           O_::mma_v(s_next, a, qb[kk]);
         }
         if constexpr (kk + D < 36) a = a_rd(std::integral_constant<int, kk + D>());
-        if constexpr (kk % 3 == 2 && kk / 3 < kDma) {
-          if constexpr (kFp8) issue_copy_fp8<kk / 3>(p, sg, t + 2, L, dbuf, wave, lane, dm);
-          else issue_copy<dma_order(kk / 3)>(p, sg, t + 2, L, dbuf, wave, lane, dm);
+        constexpr int cm = (kk - kCopyFirst) / kCopyStride;  // the copy of this step, if any
+        if constexpr (kk >= kCopyFirst && (kk - kCopyFirst) % kCopyStride == 0 && cm < kDma) {
+          if constexpr (kFp8) issue_copy_fp8<cm>(p, sg, t + 2, L, dbuf, wave, lane, dm);
+          else issue_copy<dma_order(cm)>(p, sg, t + 2, L, dbuf, wave, lane, dm);
         }
         if constexpr (kk >= kTrAt && kk - kTrAt < kPvDepth) b_issue(tr[kk - kTrAt], std::integral_constant<int, kk - kTrAt>());
         __builtin_amdgcn_sched_barrier(0);
