@@ -238,6 +238,11 @@ int run(const la_decode_args* a, hipStream_t stream) {
   const la_mla_config& c = a->cfg;
   const int64_t tokens = (int64_t)a->num_seqs * a->queries_per_seq;
   if (plan.mfma) p.q_prep = ws + plan.q_prep_off;
+  // Few query rows leave most CUs idle in the full-row merge: split it over
+  // the two latent halves, which add into the output; the absorb kernel,
+  // which runs first, zeroes it.
+  const bool merge_halves =
+      plan.proj_mfma && plan.mfma && plan.absorb_prep && merge_project_blocks(p) < cu_count();
   if (a->q_nope) {
     hipError_t e = hipSuccess;
     if (plan.absorb_prep) {
@@ -245,7 +250,8 @@ int run(const la_decode_args* a, hipStream_t stream) {
       // q_prep in the MFMAs' 16-bit type: fp16 for an fp16 cache, bf16 otherwise
       e = launch_absorb_mfma(a->q_nope, a->W_UK, a->w_uk_dtype, p.q_prep, p.kv_dtype == LA_DTYPE_F16 ? 2 : 1,
                              a->q_rope, p.scale_log2, c.qk_rope_head_dim, (int)tokens, c.num_heads,
-                             c.qk_nope_head_dim, c.kv_lora_rank, a->queries_per_seq, stream);
+                             c.qk_nope_head_dim, c.kv_lora_rank, a->queries_per_seq, stream,
+                             merge_halves ? a->output : nullptr, merge_halves ? tokens * c.num_heads * c.v_head_dim : 0);
     } else {
       float* qa = reinterpret_cast<float*>(ws + plan.q_abs_off);
       e = plan.absorb_mfma ? launch_absorb_mfma(a->q_nope, a->W_UK, a->w_uk_dtype, qa, 0, nullptr, 1.f, 0,
@@ -281,7 +287,8 @@ int run(const la_decode_args* a, hipStream_t stream) {
     }
     if (e != hipSuccess) return finish(e);
   }
-  return finish(plan.proj_mfma ? launch_combine_project_mfma(p, stream) : launch_combine_project(p, stream));
+  return finish(plan.proj_mfma ? launch_combine_project_mfma(p, stream, merge_halves)
+                                : launch_combine_project(p, stream));
 }
 
 la_decode_args shared_cache_args(const void* kv_cache, int kv_dtype, int seq_len, int batch, const float* q_absorbed,

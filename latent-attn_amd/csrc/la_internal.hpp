@@ -313,13 +313,19 @@ bool absorb_mfma_supported(int w_dtype, int nh, int dn, int dc);
 // [q_abs | q_rope] * scale in the operand-order layout, as prep_q_kernel
 // writes it; token t is query t % qps of sequence t / qps (qps = tokens per
 // sequence, used by modes 1 / 2 only).
+// zero_out (optional): zero_n floats the kernel zeroes, for a merge that adds
+// its latent halves into the output.
 hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype, void* out, int out_mode,
                               const float* q_rope, float scale, int dR, int tokens, int nh, int dn, int dc, int qps,
-                              hipStream_t stream);
+                              hipStream_t stream, float* zero_out = nullptr, int64_t zero_n = 0);
 bool project_mfma_supported(const DecodeProblem& p);
+// Workgroups of the full-row merge + projection launch.
+int merge_project_blocks(const DecodeProblem& p);
 // Merge of the split partials and W_UV projection in one kernel (the merged
-// rows stay in LDS: no workspace).
-hipError_t launch_combine_project_mfma(const DecodeProblem& p, hipStream_t stream);
+// rows stay in LDS: no workspace). halves: one workgroup per latent half,
+// which adds its product into p.out with atomics: p.out must be zero (fp16
+// partials only).
+hipError_t launch_combine_project_mfma(const DecodeProblem& p, hipStream_t stream, bool halves = false);
 
 // q_abs = q_nope . W_UK per head.
 hipError_t launch_absorb(const float* q_nope, const void* W_UK, int w_dtype, float* q_abs, int tokens, int nh, int dn,

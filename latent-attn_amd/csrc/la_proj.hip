@@ -21,7 +21,10 @@
 //          consecutive rows i per lane) comes from ds_read_b64_tr_b16.
 // merge + project: merge_project_kernel, one block of 8 waves per (weight
 //          head, 16 query rows): the log-sum-exp merge of the partial slots
-//          into LDS, then the W_UV projection of the merged rows.
+//          into LDS, then the W_UV projection of the merged rows. With fewer
+//          such blocks than CUs (a few query rows), merge_project_half_kernel
+//          splits each over the two latent halves, which add into the output
+//          (zeroed by the absorb kernel of the same call).
 #include "la_internal.hpp"
 
 #include <type_traits>
@@ -91,7 +94,8 @@ template <typename WT, int NKS>
 __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restrict__ q_nope, const WT* __restrict__ W,
                                                           void* __restrict__ out, int out_mode,
                                                           const float* __restrict__ q_rope, float scale, int dR,
-                                                          int tokens, int nh, int dn, int dc, int qps) {
+                                                          int tokens, int nh, int dn, int dc, int qps,
+                                                          float* __restrict__ zero_out, int64_t zero_n) {
   typedef Mma<WT> M;
   typedef typename M::vec vec;
   __shared__ __attribute__((aligned(16))) char wt[128 * kAbsRowBytes];  // dn <= 128 rows
@@ -108,6 +112,11 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
   const int grp = x + 8 * (k / gb), j = k % gb;  // (tb, 8-head group) group, block j in it
   const int tb = grp / nh8;
   const int h = 8 * (grp - tb * nh8) + (j & 7), cb = j >> 3, t0 = tb * 32;
+  // zero_out: the decode output, which a latent-half merge adds into (every
+  // block, before its early return, zeroes a grid-stride share)
+  if (zero_out)
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < zero_n; i += (int64_t)gridDim.x * 256)
+      zero_out[i] = 0.f;
   if (t0 >= tokens || h >= nh) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int nks = NKS > 0 ? NKS : dn / 16;  // <= 8
@@ -298,6 +307,16 @@ struct SlotRow<false> {
   }
 };
 
+// One fp16 slot's 4 columns of this lane (half-row merge).
+struct SlotRowHalf {
+  f16x4 h;
+  __device__ void load(const void* rowp) { h = *reinterpret_cast<const f16x4*>(rowp); }
+  __device__ void fma(float w, f32x4& o0, f32x4&) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o0[e] += w * (float)h[e];
+  }
+};
+
 // Log-sum-exp merge of split partial slots:
 //   O = sum_s 2^(lse_s - M) (O/l)_s / sum_s 2^(lse_s - M),  M = max_s lse_s.
 // F16 (MFMA attention kernel): slot rows hold the numerator N_s = sum 2^(s-m_s) V
@@ -308,6 +327,8 @@ struct SlotRow<false> {
 // s = g, g + G, g + 2G, ... of row t, each weighted and divided by the sum
 // over ALL slots of the row, into this lane's 8 latent columns 8 lane ..
 // 8 lane + 7 (one wave per task), so the G tasks of a row sum to its merged O.
+// A half-row merge (fp16 slots) covers only the latent half c: 4 columns
+// 256 c + 4 lane .. +3 per lane, weighted with that half's row scale.
 // Rows past the batch and empty sequences give 0.
 struct MergeTask {
   int n = 0;       // slots of the row
@@ -337,19 +358,22 @@ __device__ inline MergeTask merge_task(const DecodeProblem& p, int t, int h, int
 // most 64 takes one memory round trip. Longer merges loop over further
 // groups of 8 rows (and of 64 slots). Lane i's weights are broadcast with
 // v_readlane.
-template <bool F16>
+// kHalf: half-row merge of latent half c (o[k][1] stays 0).
+template <bool F16, bool kHalf = false>
 __device__ inline void merge_tasks(const DecodeProblem& p, const int (&t)[2], int h, int g, int G, int lane,
-                                   f32x4 (&o)[2][2]) {
+                                   f32x4 (&o)[2][2], int c = 0) {
+  static_assert(F16 || !kHalf, "half-row merges read fp16 slots");
   typedef typename std::conditional<F16, _Float16, float>::type PT;
+  typedef typename std::conditional<kHalf, SlotRowHalf, SlotRow<F16>>::type SR;
   const int64_t sstride = (int64_t)p.Hq * kDcP;
   MergeTask mt[2];
   const PT* src[2];
-  SlotRow<F16> d[2][8];
+  SR d[2][8];
   float ls_all[2], ls_own[2], m_own[2], sa_own[2], sb_own[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     mt[k] = merge_task(p, t[k], h, g, G);
-    src[k] = reinterpret_cast<const PT*>(p.part_o) + mt[k].row0 * kDcP + 8 * lane;
+    src[k] = reinterpret_cast<const PT*>(p.part_o) + mt[k].row0 * kDcP + (kHalf ? 256 * c + 4 * lane : 8 * lane);
 #pragma unroll
     for (int u = 0; u < 8; ++u)
       if (u < mt[k].ns) d[k][u].load(src[k] + (int64_t)(g + G * u) * sstride);
@@ -363,8 +387,8 @@ __device__ inline void merge_tasks(const DecodeProblem& p, const int (&t)[2], in
     ls_own[k] = own ? p.part_lse[pr] : -INFINITY;
     if constexpr (F16) {
       m_own[k] = own ? p.part_m[pr] : -INFINITY;
-      sa_own[k] = own ? p.part_scale[2 * pr] : 0.f;
-      sb_own[k] = own ? p.part_scale[2 * pr + 1] : 0.f;
+      sa_own[k] = own ? p.part_scale[2 * pr + (kHalf ? c : 0)] : 0.f;
+      sb_own[k] = own ? p.part_scale[2 * pr + (kHalf ? c : 1)] : 0.f;
     }
   }
 #pragma unroll
@@ -391,15 +415,15 @@ __device__ inline void merge_tasks(const DecodeProblem& p, const int (&t)[2], in
         ls = ok ? p.part_lse[pr] : -INFINITY;
         if constexpr (F16) {
           mm = ok ? p.part_m[pr] : -INFINITY;
-          sa = ok ? p.part_scale[2 * pr] : 0.f;
-          sb = ok ? p.part_scale[2 * pr + 1] : 0.f;
+          sa = ok ? p.part_scale[2 * pr + (kHalf ? c : 0)] : 0.f;
+          sb = ok ? p.part_scale[2 * pr + (kHalf ? c : 1)] : 0.f;
         }
       }
       float wlo, whi;
       if constexpr (F16) {
         const float a = exp2f(mm - mx) * inv;  // 0 for lanes past the task's slots
-        wlo = a * sa;  // columns 0..255 (lanes 0..31)
-        whi = a * sb;  // columns 256..511 (lanes 32..63)
+        wlo = a * sa;  // columns 0..255 (lanes 0..31); half c: all lanes
+        whi = a * sb;  // columns 256..511 (lanes 32..63); half c: all lanes
       } else {
         wlo = whi = exp2f(ls - mx) * inv;
       }
@@ -543,6 +567,107 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
   }
 }
 
+// Merge + W_UV projection over one latent half, for launches with fewer
+// (head, row block) workgroups than CUs (a few query rows): one workgroup of
+// 8 waves per (head h, 16 query rows, latent half c) merges the half rows
+// (fp16 slots, 512 B each) and multiplies them by W_UV's columns 256 c ..
+// 256 c + 255 (64 KB per head), so twice as many workgroups move half the
+// bytes each. Both halves add their products into out with float atomics;
+// absorb_mfma_kernel zeroes out earlier in the same call, and two addends
+// onto zero give fl(a + b) in either order, so the result does not depend on
+// which half lands first.
+constexpr int kMPHPitch = 256 + 8;  // 16-bit elements per LDS operand row (528 B: 16 B past 2 x 256)
+constexpr int kMPHSum = 256 + 4;    // floats per LDS row of a slot-group sum
+
+template <typename WT>
+__global__ __launch_bounds__(kMPWaves * 64) void merge_project_half_kernel(DecodeProblem p) {
+  typedef Mma16<WT> M;
+  typedef typename M::vec vec;
+  typedef typename Mma<WT>::elem E;
+  typedef typename std::conditional<std::is_same<WT, __half>::value, f16x4, bf16x4>::type vec4;
+  constexpr float kLoScale = Mma<WT>::kLoScale;
+  __shared__ __attribute__((aligned(16))) short oh[kMPRows * kMPHPitch];  // merged O half rows, high parts
+  __shared__ __attribute__((aligned(16))) short ol[kMPRows * kMPHPitch];  // and residuals
+  __shared__ __attribute__((aligned(16))) float gp[kMPWaves * kMPHSum];   // slot-group sums
+  const int R = p.num_seqs * p.qps;
+  const int nrb = (R + kMPRows - 1) / kMPRows;
+  // id = 8 (2 (head / 8 * nrb + row block) + c) + head % 8: both halves of a
+  // (head, row block) run on one XCD
+  const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+  const int c = k & 1, k2 = k >> 1;
+  const int h = (k2 / nrb) * 8 + x, rb = k2 % nrb;
+  if (h >= p.nh) return;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int rows = min(kMPRows, R - rb * kMPRows);
+
+  // W_UV operands: B[k = 32 ks + 8 (lane / 16) + j][n = lane % 16]
+  //              = W_UV[h dv + 16 wave + lane % 16][256 c + 32 ks + 8 (lane / 16) + j]
+  const WT* wrow = reinterpret_cast<const WT*>(p.W_UV) + ((int64_t)h * p.dv + 16 * wave + (lane & 15)) * kDcP +
+                   256 * c + 8 * (lane >> 4);
+  vec bw[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) bw[ks] = __builtin_bit_cast(vec, *reinterpret_cast<const i16x8*>(wrow + 32 * ks));
+
+  // row r, columns c0 .. c0 + 3 of the half -> high and low operand rows
+  auto put4 = [&](int r, int c0, const f32x4& v) {
+    vec4 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const E hv = (E)v[e];
+      hi[e] = hv;
+      lo[e] = (E)((v[e] - (float)hv) * kLoScale);
+    }
+    *reinterpret_cast<vec4*>(&oh[r * kMPHPitch + c0]) = hi;
+    *reinterpret_cast<vec4*>(&ol[r * kMPHPitch + c0]) = lo;
+  };
+  f32x4 o[2][2];
+  if (rows >= kMPWaves) {
+    const int t[2] = {rb * kMPRows + wave, wave + kMPWaves < rows ? rb * kMPRows + wave + kMPWaves : -1};
+    merge_tasks<true, true>(p, t, h, 0, 1, lane, o, c);
+    put4(wave, 4 * lane, o[0][0]);
+    put4(wave + kMPWaves, 4 * lane, t[1] >= 0 ? o[1][0] : f32x4{0.f, 0.f, 0.f, 0.f});
+    __syncthreads();
+  } else {
+    const int G = kMPWaves / rows;
+    const int r = wave / G, g = wave % G;
+    const int t[2] = {r < rows ? rb * kMPRows + r : -1, -1};
+    merge_tasks<true, true>(p, t, h, g, G, lane, o, c);
+    *reinterpret_cast<f32x4*>(&gp[wave * kMPHSum + 4 * lane]) = o[0][0];
+    __syncthreads();
+    // O half row r = sum of the G group rows of waves r G .. r G + G - 1; the
+    // block's other rows are zero
+    for (int i = tid; i < kMPRows * 64; i += kMPWaves * 64) {
+      const int rr = i / 64, c4 = i % 64;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (rr < rows)
+        for (int q = 0; q < G; ++q) v += *reinterpret_cast<const f32x4*>(&gp[(rr * G + q) * kMPHSum + 4 * c4]);
+      put4(rr, 4 * c4, v);
+    }
+    __syncthreads();
+  }
+
+  // A[m = lane % 16][k = 32 ks + 8 (lane / 16) + j] = O[m][256 c + k] (high, low)
+  f32x4 acc_hi = {}, acc_lo = {};
+  const int a0 = (lane & 15) * kMPHPitch + 8 * (lane >> 4);
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    const vec hi = *reinterpret_cast<const vec*>(&oh[a0 + 32 * ks]);
+    const vec lo = *reinterpret_cast<const vec*>(&ol[a0 + 32 * ks]);
+    acc_hi = M::mma(hi, bw[ks], acc_hi);
+    acc_lo = M::mma(lo, bw[ks], acc_lo);
+  }
+  // D[m = 4 (lane / 16) + i][n = lane % 16], added into the zeroed output
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * (lane >> 4) + i;
+    if (r < rows) {
+      const int t = rb * kMPRows + r;
+      const int64_t orow = (int64_t)(t / p.qps) * p.Hq + (t % p.qps) * p.nh + h;
+      atomicAdd(&p.out[orow * p.dv + 16 * wave + (lane & 15)], acc_hi[i] + acc_lo[i] * (1.f / kLoScale));
+    }
+  }
+}
+
 }  // namespace
 
 bool absorb_mfma_supported(int w_dtype, int nh, int dn, int dc) {
@@ -552,7 +677,7 @@ bool absorb_mfma_supported(int w_dtype, int nh, int dn, int dc) {
 
 hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype, void* out, int out_mode,
                               const float* q_rope, float scale, int dR, int tokens, int nh, int dn, int dc, int qps,
-                              hipStream_t stream) {
+                              hipStream_t stream, float* zero_out, int64_t zero_n) {
   if (out_mode != 0 && (dc + dR != kQPrepRow || qps <= 0)) return hipErrorInvalidValue;
   // one block per (token block, head, column block), ordered for the XCDs:
   // groups of (token block, 8 heads) with 8 * (dc / 128) blocks each
@@ -562,11 +687,11 @@ hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype
   if (w_dtype == LA_DTYPE_BF16) {
     auto k = d128 ? absorb_mfma_kernel<__hip_bfloat16, 8> : absorb_mfma_kernel<__hip_bfloat16, 0>;
     hipLaunchKernelGGL(k, grid, dim3(256), 0, stream, q_nope, reinterpret_cast<const __hip_bfloat16*>(W_UK), out,
-                       out_mode, q_rope, scale, dR, tokens, nh, dn, dc, qps);
+                       out_mode, q_rope, scale, dR, tokens, nh, dn, dc, qps, zero_out, zero_n);
   } else {
     auto k = d128 ? absorb_mfma_kernel<__half, 8> : absorb_mfma_kernel<__half, 0>;
     hipLaunchKernelGGL(k, grid, dim3(256), 0, stream, q_nope, reinterpret_cast<const __half*>(W_UK), out, out_mode,
-                       q_rope, scale, dR, tokens, nh, dn, dc, qps);
+                       q_rope, scale, dR, tokens, nh, dn, dc, qps, zero_out, zero_n);
   }
   return hipGetLastError();
 }
@@ -576,10 +701,25 @@ bool project_mfma_supported(const DecodeProblem& p) {
          (reinterpret_cast<uintptr_t>(p.W_UV) & 15) == 0;
 }
 
-hipError_t launch_combine_project_mfma(const DecodeProblem& p, hipStream_t stream) {
+int merge_project_blocks(const DecodeProblem& p) {
+  const int R = p.num_seqs * p.qps;
+  return 8 * ((p.nh + 7) / 8) * ((R + kMPRows - 1) / kMPRows);
+}
+
+hipError_t launch_combine_project_mfma(const DecodeProblem& p, hipStream_t stream, bool halves) {
   const int R = p.num_seqs * p.qps;
   if (R == 0) return hipSuccess;
   const int nrb = (R + kMPRows - 1) / kMPRows;
+  if (halves) {
+    if (!p.part_f16) return hipErrorInvalidValue;
+    // id = 8 (2 (head / 8 * nrb + row block) + half) + head % 8
+    const dim3 grid((unsigned)(2 * merge_project_blocks(p)));
+    if (p.wuv_dtype == LA_DTYPE_BF16)
+      hipLaunchKernelGGL(merge_project_half_kernel<__hip_bfloat16>, grid, dim3(kMPWaves * 64), 0, stream, p);
+    else
+      hipLaunchKernelGGL(merge_project_half_kernel<__half>, grid, dim3(kMPWaves * 64), 0, stream, p);
+    return hipGetLastError();
+  }
   // id = 8 (head / 8 * nrb + row block) + head % 8
   const dim3 grid((unsigned)(8 * ((p.nh + 7) / 8) * nrb));
   if (p.wuv_dtype == LA_DTYPE_BF16) {

@@ -109,6 +109,20 @@ def test_config2_single_sequence(cuda, abi):
     assert_close(out[0], naive, "bf16", "cfg2 vs naive decompress-then-attend")
 
 
+def test_config2_merge_halves_repeat_bitwise(cuda, abi):
+    """At B = 1 the full-row merge would launch 128 workgroups for 256 CUs, so
+    the launch merges each latent half in its own workgroup and both add into
+    the output (zeroed by the absorb kernel) with float atomics. Two addends
+    onto zero give fl(a + b) in either order: repeated calls are bitwise equal."""
+    lib, capi = abi
+    inp = bench.build_inputs("cfg2", cuda)
+    outs = [_run(inp, lib, capi) for _ in range(4)]
+    print("[cfg2] four calls, merge over latent halves", flush=True)
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    assert_close(outs[0][0], _oracle_seq(inp, 0), "bf16", "cfg2 (latent-half merge) vs absorbed oracle")
+
+
 def test_config2_plan_keeps_partials_below_cache(cuda, abi):
     """At B = 1 the MFMA split plan gives every chunk at least ceil(Hq*512/576)
     rows (128 at Hq = 128), so the fp16 partial rows it writes (Hq x 1 KB per
