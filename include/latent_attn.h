@@ -121,7 +121,9 @@ typedef struct la_decode_args {
    * the longest sequence). Positions past it read the last row instead of
    * faulting. */
   int64_t rope_rows;
-  float* output; /* (tokens, num_heads, v_head_dim) f32 */
+  /* (tokens, num_heads, v_head_dim) f32; must not overlap an input (a call
+   * with few query rows zeroes it first and adds partial products into it) */
+  float* output;
   la_mla_config cfg;
   /* scratch for split partials (and the absorbed query when q_nope is given).
    * NULL: the library takes stream-ordered memory (hipMallocAsync) and returns
