@@ -164,6 +164,27 @@ def test_split_invariance(cuda, chunk_rows, variant):
     assert_close(out.cpu().numpy(), ref, "bf16", f"chunk_rows={chunk_rows} variant={variant}")
 
 
+@pytest.mark.parametrize("B,S,picks", [(17, 4096, (0, 8, 16)), (1, 32768, (0,))])
+def test_merge_over_many_slots(cuda, B, S, picks):
+    """32-row chunks give every query row S/32 partial slots (plus one where a
+    chunk straddles two sequences). B = 17 (272 row blocks x heads: the
+    full-row merge) has 128 slots per row, one wave per row: its slot weights
+    come in two blocks of 64. B = 1 (the latent-half merge, a row's slots split
+    over 8 waves) has 1,024 slots, 128 per wave: two blocks as well, and the
+    row maximum and denominator loop past the first 64 slots."""
+    cfg = MLAConfig.deepseek_v2()
+    kv = make_cache((B, S), cfg, "bf16", 26, cuda)
+    W_UK, W_UV = make_weights(cfg, "bf16", 27, cuda)
+    q_nope, q_rope = make_queries((B,), cfg, 28, cuda)
+    cos, sin = rope(S, cfg, cuda)
+    out = F.mla_decode(kv, q_nope, q_rope, W_UK, W_UV, cos, sin, cfg, chunk_rows=32).cpu().numpy()
+    print(f"[many slots] B={B} S={S} chunk_rows=32: {S // 32} slots per row", flush=True)
+    assert np.isfinite(out).all()
+    for b in picks:
+        ref = oracle_decode(kv[b], [0, S], q_nope[b:b + 1], q_rope[b:b + 1], W_UK, W_UV, cos, sin, cfg)
+        assert_close(out[b], ref[0], "bf16", f"B={B} S={S} seq {b}, {S // 32} slots per row")
+
+
 @pytest.mark.parametrize("variant", [1, 2])
 def test_ragged_with_empty_and_short_sequences(cuda, variant):
     cfg = MLAConfig.deepseek_v2()
