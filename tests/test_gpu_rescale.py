@@ -77,3 +77,42 @@ def test_rescale_paged(cuda, dtype, chunk_rows):
     torch.cuda.synchronize()
     ref = oracle(kv, qa, qr, W_UV, cos, sin, [S] * B)
     assert_close(out.cpu().numpy(), ref, dtype, f"rescale paged {dtype} chunk {chunk_rows}")
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_rescale_fp8_cache(cuda, paged):
+    """The staircase in an FP8 E4M3 cache (the fp8 instantiations of the
+    kernel: rows expanded to bf16 in LDS). The staircase columns are halved
+    (48 x tier, exact in E4M3, whose largest value is 448) and the query
+    weights on them doubled, so the scores climb exactly as in the 16-bit
+    cases; the other values are the fp8 codes of the random part, and the
+    oracle reads the same codes."""
+    cfg = MLAConfig.deepseek_v2()
+    kv16, qa, qr = staircase_case(B, S, "bf16", 5, cuda)
+    kv8 = (kv16.float() * 0.5).to(torch.float8_e4m3fn)
+    qa = qa.clone()
+    qa[:, :, 0:2] *= 2.0
+    kv_np = mo.fp8_e4m3_decode(kv8.view(torch.uint8).cpu().numpy())
+    assert np.array_equal(kv_np[:, :, 0:2], to_np(kv16)[:, :, 0:2] * 0.5), "staircase columns exact in E4M3"
+    _, W_UV = make_weights(cfg, "bf16", 6, cuda)
+    if paged:
+        cap, bs = 3072, 64
+        bps = cap // bs
+        full = torch.zeros(B, cap, 576, dtype=torch.uint8, device=cuda)
+        full[:, :S] = kv8.view(torch.uint8)
+        perm = torch.from_numpy(np.random.RandomState(9).permutation(B * bps).astype(np.int32)).to(cuda)
+        pool = torch.empty(B * cap, 576, dtype=torch.float8_e4m3fn, device=cuda)
+        pool.view(torch.uint8).view(B * bps, bs, 576)[perm.long()] = full.view(B * bps, bs, 576)
+        table = perm.view(B, bps)
+        lens = torch.full((B,), S, dtype=torch.int32, device=cuda)
+        cos, sin = rope(cap, cfg, cuda)
+        out = F.mla_decode_absorbed(pool, qa, qr, W_UV, cos, sin, cfg, seq_lens=lens, kernel_variant=2,
+                                    block_table=table, block_size=bs)
+    else:
+        cos, sin = rope(S, cfg, cuda)
+        out = F.mla_decode_absorbed(kv8, qa, qr, W_UV, cos, sin, cfg, kernel_variant=2)
+    torch.cuda.synchronize()
+    packed = np.concatenate([kv_np[b] for b in range(B)]).astype(np.float64)
+    ref = mo.decode_sequences(packed, [b * S for b in range(B + 1)], to_np(qa), to_np(qr), to_np(W_UV),
+                              to_np(cos)[:S], to_np(sin)[:S], D)
+    assert_close(out.cpu().numpy(), ref, "bf16", f"rescale fp8 {'paged' if paged else 'contiguous'}")
