@@ -239,10 +239,13 @@ int run(const la_decode_args* a, hipStream_t stream) {
   const int64_t tokens = (int64_t)a->num_seqs * a->queries_per_seq;
   if (plan.mfma) p.q_prep = ws + plan.q_prep_off;
   // Few query rows leave most CUs idle in the full-row merge: split it over
-  // the two latent halves, which add into the output; the absorb kernel,
-  // which runs first, zeroes it.
-  const bool merge_halves =
-      plan.proj_mfma && plan.mfma && plan.absorb_prep && merge_project_blocks(p) < cu_count();
+  // the two latent halves, which add into the output. The kernel that writes
+  // the attention kernel's 16-bit queries (the absorb kernel, or prep_q when
+  // the queries come absorbed) runs first and zeroes the output.
+  const bool merge_halves = plan.proj_mfma && plan.mfma && (plan.absorb_prep || plan.num_chunks > 0) &&
+                            merge_project_blocks(p) < cu_count();
+  float* const zero_out = merge_halves ? a->output : nullptr;
+  const int64_t zero_n = merge_halves ? tokens * c.num_heads * c.v_head_dim : 0;
   if (a->q_nope) {
     hipError_t e = hipSuccess;
     if (plan.absorb_prep) {
@@ -250,8 +253,7 @@ int run(const la_decode_args* a, hipStream_t stream) {
       // q_prep in the MFMAs' 16-bit type: fp16 for an fp16 cache, bf16 otherwise
       e = launch_absorb_mfma(a->q_nope, a->W_UK, a->w_uk_dtype, p.q_prep, p.kv_dtype == LA_DTYPE_F16 ? 2 : 1,
                              a->q_rope, p.scale_log2, c.qk_rope_head_dim, (int)tokens, c.num_heads,
-                             c.qk_nope_head_dim, c.kv_lora_rank, a->queries_per_seq, stream,
-                             merge_halves ? a->output : nullptr, merge_halves ? tokens * c.num_heads * c.v_head_dim : 0);
+                             c.qk_nope_head_dim, c.kv_lora_rank, a->queries_per_seq, stream, zero_out, zero_n);
     } else {
       float* qa = reinterpret_cast<float*>(ws + plan.q_abs_off);
       e = plan.absorb_mfma ? launch_absorb_mfma(a->q_nope, a->W_UK, a->w_uk_dtype, qa, 0, nullptr, 1.f, 0,
@@ -269,7 +271,7 @@ int run(const la_decode_args* a, hipStream_t stream) {
   p.part_m = plan.mfma ? p.part_scale + (size_t)plan.num_slots * p.Hq * 2 : nullptr;
   if (plan.num_chunks > 0) {
     if (plan.mfma && !plan.absorb_prep) {
-      hipError_t e = launch_prep_q(p, stream);
+      hipError_t e = launch_prep_q(p, stream, zero_out, zero_n);
       if (e != hipSuccess) return finish(e);
     }
     // the optional events bracket the attention kernel alone

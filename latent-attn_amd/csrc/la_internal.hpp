@@ -302,7 +302,8 @@ bool mfma_supported(const DecodeProblem& p);
 int mfma_heads_per_group();
 int mfma_max_chunk_rows();
 // Fills p.q_prep from p.q_abs and p.q_rope (MFMA path only).
-hipError_t launch_prep_q(const DecodeProblem& p, hipStream_t stream);
+// zero_out (optional): zero_n floats zeroed for a latent-half merge.
+hipError_t launch_prep_q(const DecodeProblem& p, hipStream_t stream, float* zero_out = nullptr, int64_t zero_n = 0);
 
 // log-sum-exp combine of the partial slots + W_UV projection into p.out.
 hipError_t launch_combine_project(const DecodeProblem& p, hipStream_t stream);

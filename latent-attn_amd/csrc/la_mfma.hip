@@ -1416,14 +1416,19 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
 // q_prep = E([q_abs[row] (dc) | q_rope[row] (dR)] * scale_log2) in the
 // operand-order layout (qprep_index); row = s * Hq + hq. One thread per 8
 // consecutive elements (72 per row for dc = 512, dR = 64), i.e. per 16-B slot.
+// zero_out: the decode output, which a latent-half merge adds into (zeroed
+// grid-stride, before the early return).
 template <typename KT>
 __global__ __launch_bounds__(256) void prep_q_kernel(const float* __restrict__ q_abs, const float* __restrict__ q_rope,
                                                      float scale, typename Ops<KT>::elem* __restrict__ out,
-                                                     int64_t rows, int Hq) {
+                                                     int64_t rows, int Hq, float* __restrict__ zero_out,
+                                                     int64_t zero_n) {
   typedef typename Ops<KT>::elem E;
   typedef typename Ops<KT>::vec vec;
   constexpr int kPer = (kDc + kDr) / 8;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (zero_out)
+    for (int64_t z = i; z < zero_n; z += (int64_t)gridDim.x * 256) zero_out[z] = 0.f;
   if (i >= rows * kPer) return;
   const int64_t row = i / kPer;
   const int j = (int)(i - row * kPer);
@@ -1500,17 +1505,18 @@ bool mfma_supported(const DecodeProblem& p) {
   return device_is_gfx950();
 }
 
-hipError_t launch_prep_q(const DecodeProblem& p, hipStream_t stream) {
+hipError_t launch_prep_q(const DecodeProblem& p, hipStream_t stream, float* zero_out, int64_t zero_n) {
   const int64_t rows = (int64_t)p.num_seqs * p.Hq;
   const int64_t threads = rows * ((kDc + kDr) / 8);
   if (threads == 0) return hipSuccess;
   const unsigned blocks = (unsigned)((threads + 255) / 256);
   if (p.kv_dtype != LA_DTYPE_F16)  // bf16 and fp8 caches run bf16 MFMAs
     hipLaunchKernelGGL(prep_q_kernel<__hip_bfloat16>, dim3(blocks), dim3(256), 0, stream, p.q_abs, p.q_rope,
-                       p.scale_log2, reinterpret_cast<Ops<__hip_bfloat16>::elem*>(p.q_prep), rows, p.Hq);
+                       p.scale_log2, reinterpret_cast<Ops<__hip_bfloat16>::elem*>(p.q_prep), rows, p.Hq, zero_out,
+                       zero_n);
   else
     hipLaunchKernelGGL(prep_q_kernel<__half>, dim3(blocks), dim3(256), 0, stream, p.q_abs, p.q_rope, p.scale_log2,
-                       reinterpret_cast<Ops<__half>::elem*>(p.q_prep), rows, p.Hq);
+                       reinterpret_cast<Ops<__half>::elem*>(p.q_prep), rows, p.Hq, zero_out, zero_n);
   return hipGetLastError();
 }
 

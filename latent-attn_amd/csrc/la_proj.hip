@@ -24,7 +24,8 @@
 //          into LDS, then the W_UV projection of the merged rows. With fewer
 //          such blocks than CUs (a few query rows), merge_project_half_kernel
 //          splits each over the two latent halves, which add into the output
-//          (zeroed by the absorb kernel of the same call).
+//          (zeroed earlier in the same call by the kernel that writes the
+//          attention kernel's 16-bit queries).
 #include "la_internal.hpp"
 
 #include <type_traits>
@@ -573,9 +574,10 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
 // (fp16 slots, 512 B each) and multiplies them by W_UV's columns 256 c ..
 // 256 c + 255 (64 KB per head), so twice as many workgroups move half the
 // bytes each. Both halves add their products into out with float atomics;
-// absorb_mfma_kernel zeroes out earlier in the same call, and two addends
-// onto zero give fl(a + b) in either order, so the result does not depend on
-// which half lands first.
+// the kernel that writes the attention kernel's 16-bit queries
+// (absorb_mfma_kernel, or prep_q_kernel for pre-absorbed queries) zeroes out
+// earlier in the same call, and two addends onto zero give fl(a + b) in
+// either order, so the result does not depend on which half lands first.
 constexpr int kMPHPitch = 256 + 8;  // 16-bit elements per LDS operand row (528 B: 16 B past 2 x 256)
 constexpr int kMPHSum = 256 + 4;    // floats per LDS row of a slot-group sum
 
