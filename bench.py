@@ -518,9 +518,33 @@ def time_mall_cold(hip, step, stream, dev, steps: int = 30, flush_mib: int = 102
             hip.hipEventDestroy(b)
             hip.hipEventDestroy(e)
         us.sort()
-        res["cold" if cold else "warm"] = {"mean_us": round(sum(us) / len(us), 2), "median_us": round(us[len(us) // 2], 2)}
+        n = len(us)
+        res["cold" if cold else "warm"] = {"mean_us": round(sum(us) / n, 2), "median_us": round(us[n // 2], 2),
+                                           "p10_us": round(us[n // 10], 2), "p90_us": round(us[(9 * n) // 10], 2)}
     del src, dst
     return {"flush_mib": flush_mib, "steps": steps, **res}
+
+
+def step_bytes(inp, ws_bytes: int, ms_step: float) -> dict:
+    """Algorithmic HBM bytes of one step beside the latent cache (the
+    secondary total): both weight matrices, queries in and outputs out, the
+    RoPE table rows the longest sequence reads, and the workspace's query and
+    partial regions (the partials written once by the attention kernel and read
+    once by the merge, the 16-bit queries written by the absorb kernel and read
+    by the attention kernel)."""
+    cfg = inp["cfg"]
+    B, H = inp["B"], cfg.num_heads
+    lens = inp["lens"]
+    b = {
+        "cache": int(inp["total"]) * BYTES_PER_POS,
+        "weights": 2 * H * cfg.kv_lora_rank * (cfg.qk_nope_head_dim + cfg.v_head_dim),
+        "queries_and_output": 4 * B * H * (cfg.qk_nope_head_dim + cfg.qk_rope_head_dim + cfg.v_head_dim),
+        "rope_tables": 2 * 4 * int(max(lens)) * (cfg.qk_rope_head_dim // 2),
+        "workspace_written_and_read": 2 * int(ws_bytes),
+    }
+    b["total"] = sum(b.values())
+    b["total_GBps"] = round(b["total"] / (ms_step * 1e-3) / 1e9, 1)
+    return b
 
 
 def config_leg(lib, capi, hip, name: str, dev, stream, steps: int = 50) -> dict:
@@ -658,6 +682,7 @@ def main():
         },
         "tokens_per_s": round(B / (ms_step * 1e-3), 1),
         "latent_cache_GBps": round(cache_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "step_bytes": step_bytes(inp, step.ws.numel(), ms_step),
         "attn_kernel_us": round(kern_avg * 1e3, 2),
         "attn_kernel_us_min_max": [round(kern_ms[0] * 1e3, 2), round(kern_ms[-1] * 1e3, 2)],
         "mfma_frac_of_bf16_peak": round(flops_attn / (kern_avg * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
