@@ -146,6 +146,17 @@ def decode_args(inp, out, capi):
     return a
 
 
+def decode_call(lib, a, stream, ev_b=None, ev_e=None, repeat: int = 0, what: str = "") -> None:
+    """One decode step: la_mla_decode, or la_mla_decode_profiled when events
+    bracket the attention kernel (launched `repeat` times back to back)."""
+    if ev_b is None and ev_e is None and repeat <= 1:
+        st = lib.la_mla_decode(ctypes.byref(a), ctypes.c_void_p(stream))
+    else:
+        st = lib.la_mla_decode_profiled(ctypes.byref(a), ctypes.c_void_p(stream), ev_b, ev_e, repeat)
+    if st != 0:
+        raise RuntimeError(f"la_mla_decode{what}: {lib.la_status_string(st).decode()} hip={lib.la_last_hip_error()}")
+
+
 def time_append(lib, hip, capi, inp, stream, calls: int = 100) -> float:
     """Microseconds per la_append_kv call: one bf16 row per sequence of the
     batch appended at its length into a capacity cache (B, calls + 8, 576),
@@ -225,10 +236,7 @@ def time_paged(lib, hip, capi, inp, out, ws, stream, bs: int = 64, steps: int = 
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
 
     def step(ev_b=None, ev_e=None, repeat=0):
-        a.decode_event_begin, a.decode_event_end, a.decode_repeat = ev_b, ev_e, repeat
-        st = lib.la_mla_decode(ctypes.byref(a), ctypes.c_void_p(stream))
-        if st != 0:
-            raise RuntimeError(f"la_mla_decode (paged): {lib.la_status_string(st).decode()}")
+        decode_call(lib, a, stream, ev_b, ev_e, repeat, " (paged)")
 
     for _ in range(20):
         step()
@@ -268,10 +276,8 @@ def time_fp8(lib, hip, capi, inp, out, stream, steps: int = 100) -> dict:
     ws8 = torch.empty(need, dtype=torch.uint8, device=kv8.device)
     a.workspace, a.workspace_bytes = ws8.data_ptr(), need
 
-    def step():
-        st = lib.la_mla_decode(ctypes.byref(a), ctypes.c_void_p(stream))
-        if st != 0:
-            raise RuntimeError(f"la_mla_decode (fp8): {lib.la_status_string(st).decode()}")
+    def step(ev_b=None, ev_e=None, repeat=0):
+        decode_call(lib, a, stream, ev_b, ev_e, repeat, " (fp8)")
 
     for _ in range(20):
         step()
@@ -287,14 +293,8 @@ def time_fp8(lib, hip, capi, inp, out, stream, steps: int = 100) -> dict:
     hip.hipEventDestroy(t0)
     hip.hipEventDestroy(t1)
 
-    def step_ev(ev_b=None, ev_e=None, repeat=0):
-        a.decode_event_begin, a.decode_event_end, a.decode_repeat = ev_b, ev_e, repeat
-        step()
-
-    kern = time_attention(hip, step_ev)
+    kern = time_attention(hip, step)
     kern_us = sum(kern) / len(kern) * 1e3
-    a.decode_event_begin = a.decode_event_end = None
-    a.decode_repeat = 0
     fp8_bytes = int(inp["total"]) * BYTES_PER_POS // 2
     return {"step_us": round(us, 2), "attn_kernel_us": round(kern_us, 2),
             "cache_frac_of_8TBps": round(fp8_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
@@ -430,12 +430,7 @@ class Stepper:
         self.a.workspace, self.a.workspace_bytes = self.ws.data_ptr(), need
 
     def __call__(self, ev_b=None, ev_e=None, repeat=0):
-        a = self.a
-        a.decode_event_begin, a.decode_event_end, a.decode_repeat = ev_b, ev_e, repeat
-        st = self.lib.la_mla_decode(ctypes.byref(a), ctypes.c_void_p(self.stream))
-        if st != 0:
-            raise RuntimeError(f"la_mla_decode: {self.lib.la_status_string(st).decode()} "
-                               f"hip={self.lib.la_last_hip_error()}")
+        decode_call(self.lib, self.a, self.stream, ev_b, ev_e, repeat)
 
 
 def settle_clocks(step, min_ms: float) -> dict:
@@ -473,7 +468,7 @@ def time_steps(hip, step, stream, K: int) -> float:
 
 def time_attention(hip, step, calls: int = 10, repeat: int = 10) -> list:
     """Attention-kernel milliseconds per launch: `calls` steps, each running
-    the attention kernel `repeat` times back to back (decode_repeat) between
+    the attention kernel `repeat` times back to back (la_mla_decode_profiled) between
     one fence-free event pair on the launch stream. An event pair around a
     single launch also times its dispatch (~5 us; in a step that dispatch
     overlaps the previous kernel), while back-to-back launches overlap their

@@ -54,7 +54,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 3
+#define LA_ABI_VERSION 4
 
 typedef enum la_status {
   LA_SUCCESS = 0,
@@ -136,15 +136,6 @@ typedef struct la_decode_args {
    *                the shape has none) */
   int32_t chunk_rows;
   int32_t kernel_variant;
-  /* optional hipEvent_t handles recorded on `stream` right before and right
-   * after the split-KV attention kernel (profiling); NULL = not recorded. */
-  void* decode_event_begin;
-  void* decode_event_end;
-  /* profiling: > 1 runs the split-KV attention kernel this many times back to
-   * back between the two events (every launch rewrites the same partial
-   * slots, so the result is unchanged), so the events time launches whose
-   * dispatch overlaps the previous one; 0 or 1 = once. */
-  int32_t decode_repeat;
   /* optional DEVICE int32 array of num_seqs lengths (as la_append_kv keeps
    * them): sequence s is the first seq_lens[s] rows of its region above
    * (clamped into it; rows past it are unfilled capacity and are not read).
@@ -229,6 +220,17 @@ size_t la_mla_decode_workspace_size(const la_decode_args* args);
 /* One decode step: [absorb] -> split-KV latent attention -> log-sum-exp
  * combine -> W_UV projection. */
 int la_mla_decode(const la_decode_args* args, void* stream);
+
+/* la_mla_decode for profilers and benchmarks that time the split-KV attention
+ * kernel alone. No counterpart in the reference. event_begin / event_end:
+ * optional hipEvent_t handles recorded on `stream` right before and right
+ * after the attention kernel (NULL = not recorded). repeat > 1 launches the
+ * attention kernel that many times back to back between the two events (each
+ * launch rewrites the same partial slots, so the result is unchanged), so the
+ * events time launches whose dispatch overlaps the previous one; 0 or 1 =
+ * once; negative = LA_ERROR_INVALID_VALUE. */
+int la_mla_decode_profiled(const la_decode_args* args, void* stream, void* event_begin, void* event_end,
+                           int32_t repeat);
 
 /* la_mla_decode without any allocation. No counterpart in the reference: for
  * callers that cannot allocate device memory (code under HIP graph capture,

@@ -70,8 +70,7 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   if (!a || !valid_cfg(&a->cfg)) return LA_ERROR_INVALID_VALUE;
   const int chunk_rows = a->chunk_rows;
   const int variant = a->kernel_variant;
-  if (chunk_rows < 0 || variant < kAuto || variant > kMfma || a->rope_rows < 0 || a->decode_repeat < 0)
-    return LA_ERROR_INVALID_VALUE;
+  if (chunk_rows < 0 || variant < kAuto || variant > kMfma || a->rope_rows < 0) return LA_ERROR_INVALID_VALUE;
   if (a->num_seqs < 0 || a->queries_per_seq < 1 || a->total_rows < 0) return LA_ERROR_INVALID_VALUE;
   if (!valid_cache_dtype(a->kv_dtype) || !valid_dtype(a->w_uv_dtype)) return LA_ERROR_INVALID_VALUE;
   const bool paged = a->block_table != nullptr;
@@ -207,7 +206,11 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   return LA_SUCCESS;
 }
 
-int run(const la_decode_args* a, hipStream_t stream) {
+// ev_b / ev_e (optional) are recorded around the attention kernel, which runs
+// max(repeat, 1) times between them.
+int run(const la_decode_args* a, hipStream_t stream, hipEvent_t ev_b = nullptr, hipEvent_t ev_e = nullptr,
+        int repeat = 1) {
+  if (repeat < 0) return LA_ERROR_INVALID_VALUE;
   DecodeProblem p;
   Plan plan;
   int st = prepare(a, &p, &plan);
@@ -275,10 +278,8 @@ int run(const la_decode_args* a, hipStream_t stream) {
       if (e != hipSuccess) return finish(e);
     }
     // the optional events bracket the attention kernel alone
-    hipEvent_t ev_b = static_cast<hipEvent_t>(a->decode_event_begin);
-    hipEvent_t ev_e = static_cast<hipEvent_t>(a->decode_event_end);
     hipError_t e = hipSuccess;
-    const int reps = a->decode_repeat > 1 ? a->decode_repeat : 1;
+    const int reps = repeat > 1 ? repeat : 1;
     if (plan.mfma && reps == 1) {
       e = launch_decode_mfma(p, stream, ev_b, ev_e);  // recorded by the launch itself
     } else {
@@ -381,6 +382,12 @@ size_t la_mla_decode_workspace_size(const la_decode_args* args) {
 }
 
 int la_mla_decode(const la_decode_args* args, void* stream) { return la::run(args, static_cast<hipStream_t>(stream)); }
+
+int la_mla_decode_profiled(const la_decode_args* args, void* stream, void* event_begin, void* event_end,
+                           int32_t repeat) {
+  return la::run(args, static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(event_begin),
+                 static_cast<hipEvent_t>(event_end), repeat);
+}
 
 int la_mla_decode_noalloc(const la_decode_args* args, void* stream) {
   la::DecodeProblem p;

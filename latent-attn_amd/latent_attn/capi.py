@@ -52,9 +52,6 @@ class DecodeArgs(ctypes.Structure):
         ("workspace_bytes", ctypes.c_size_t),
         ("chunk_rows", ctypes.c_int32),
         ("kernel_variant", ctypes.c_int32),
-        ("decode_event_begin", ctypes.c_void_p),
-        ("decode_event_end", ctypes.c_void_p),
-        ("decode_repeat", ctypes.c_int32),
         ("seq_lens", ctypes.c_void_p),
         ("block_table", ctypes.c_void_p),
         ("block_size", ctypes.c_int32),
@@ -113,6 +110,8 @@ def load() -> ctypes.CDLL:
     lib.la_mla_decode.argtypes = [ctypes.POINTER(DecodeArgs), vp]
     lib.la_mla_decode_noalloc.restype = i32
     lib.la_mla_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), vp]
+    lib.la_mla_decode_profiled.restype = i32
+    lib.la_mla_decode_profiled.argtypes = [ctypes.POINTER(DecodeArgs), vp, vp, vp, ctypes.c_int32]
     lib.la_mla_decode_noalloc_max_bytes.restype = sz
     lib.la_mla_decode_noalloc_max_bytes.argtypes = []
     lib.la_fused_mla.restype = i32

@@ -23,7 +23,7 @@ def test_library_exports_header_symbols():
     assert {"la_mla_decode", "la_fused_mla", "la_batched_fused_mla", "la_absorb_q", "la_append_kv"} <= set(names)
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.la_abi_version() == 3
+    assert lib.la_abi_version() == 4
 
 
 def test_ctypes_structs_match_the_header(tmp_path):
@@ -149,6 +149,16 @@ def test_decode_rejects_bad_arguments(field, value):
     lib = capi.load()
     a = _args(**{field: value})
     assert lib.la_mla_decode(ctypes.byref(a), None) == capi.LA_ERROR_INVALID_VALUE
+
+
+def test_profiled_decode_rejects_a_negative_repeat():
+    """la_mla_decode_profiled checks its repeat count before any device work
+    (and, like la_mla_decode, every descriptor field)."""
+    lib = capi.load()
+    a = _args()
+    assert lib.la_mla_decode_profiled(ctypes.byref(a), None, None, None, -1) == capi.LA_ERROR_INVALID_VALUE
+    a = _args(queries_per_seq=0)
+    assert lib.la_mla_decode_profiled(ctypes.byref(a), None, None, None, 10) == capi.LA_ERROR_INVALID_VALUE
 
 
 def test_decode_rejects_bad_config():
