@@ -185,6 +185,33 @@ def test_merge_over_many_slots(cuda, B, S, picks):
         assert_close(out[b], ref[0], "bf16", f"B={B} S={S} seq {b}, {S // 32} slots per row")
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_other_head_dims(cuda, dtype):
+    """A shape other than DeepSeek's (kv_lora_rank 256, qk_rope_head_dim 32,
+    qk_nope_head_dim 64, v_head_dim 96, 12 heads; MLAConfig allows any
+    positive dims with an even rope dim, src/mla_config.cuh:35-40) runs on the
+    VALU kernels (absorb on MFMA, whose 128-column blocks still fit), over a
+    ragged batch with a one-position sequence, against the oracle; the naive
+    path on one sequence too."""
+    cfg = MLAConfig(1024, 256, 64, 32, 12, 96)
+    lens = [100, 1, 333]
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    kv = make_cache((int(offs[-1]),), cfg, dtype, 36, cuda)
+    W_UK, W_UV = make_weights(cfg, dtype, 37, cuda)
+    q_nope, q_rope = make_queries((len(lens),), cfg, 38, cuda)
+    cos, sin = rope(max(lens), cfg, cuda)
+    ref = oracle_decode(kv, offs, q_nope, q_rope, W_UK, W_UV, cos, sin, cfg)
+    off_t = torch.tensor(offs, dtype=torch.int32, device=cuda)
+    out = F.mla_decode(kv, q_nope, q_rope, W_UK, W_UV, cos, sin, cfg, seq_offsets=off_t).cpu().numpy()
+    assert_close(out, ref, dtype, f"dims 256/32/64/96 x 12 heads ({dtype})")
+    d = dims(cfg)
+    kv2 = kv[int(offs[2]):int(offs[3])]
+    naive = F.naive_mla(kv2, W_UK, W_UV, q_nope[2], q_rope[2], cos, sin, cfg).cpu().numpy()
+    ref2 = mo.naive_mla(to_np(kv2), to_np(W_UK), to_np(W_UV), to_np(q_nope[2]), to_np(q_rope[2]), to_np(cos),
+                        to_np(sin), d)
+    assert_close(naive, ref2, "f32" if dtype == "f32" else dtype, f"naive, other dims ({dtype})")
+
+
 @pytest.mark.parametrize("variant", [1, 2])
 def test_ragged_with_empty_and_short_sequences(cuda, variant):
     cfg = MLAConfig.deepseek_v2()
