@@ -371,6 +371,14 @@ template <typename T>
 __device__ inline void lds_st(lchar* L, uint32_t off, T v) {
   *reinterpret_cast<__attribute__((address_space(3))) T*>(L + off) = v;
 }
+// 16-B global store at device scope (sc1): written through this XCD's L2 to
+// the device's coherence point. The partial slots go out this way, so the
+// release at the end of the grid finds no dirty partial lines left in the L2s
+// to write back (attention -2 us at config 3), and the merge kernel, on any
+// XCD, still reads them from the infinity cache (its time is unchanged).
+__device__ inline void st_global_dev16(void* p, i16x8 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
 // ds_read_b64_tr_b16 as inline asm: the builtin makes the compiler assume the
 // read may alias the in-flight HBM->LDS copies and drain vmcnt before it. OFF
 // is the instruction's immediate byte offset. The result must not be used
@@ -1405,7 +1413,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         constexpr int j = decltype(j_c)::value;
         const int r = 2 * j + (lr >> 5);                       // staged row
         const int hb = r < 32 ? 32 * wave + r : 32 * pw + (r - 32);  // head within the group
-        if (hb < hg_heads) *reinterpret_cast<i16x8*>(obase + (uint32_t)(hb * kDc)) = xr[j];
+        if (hb < hg_heads) st_global_dev16(obase + (uint32_t)(hb * kDc), xr[j]);
       });
     }
     lo = seg_hi;
