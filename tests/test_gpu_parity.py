@@ -339,3 +339,40 @@ def test_absorb_q_matches_oracle(cuda, wdtype, tokens):
     ref = mo.absorb_q(to_np(q_nope), to_np(W_UK), dims(cfg))
     assert out.shape == (tokens, 128, 512) and out.dtype == torch.float32
     assert_close(out.cpu().numpy(), ref, "f32", f"absorb_q {wdtype} x{tokens}")
+
+
+@pytest.mark.parametrize("chunk_rows", [1, 7])
+@pytest.mark.parametrize("variant", [1, 2])
+def test_chunks_shorter_than_a_tile(cuda, chunk_rows, variant):
+    """Explicit chunk sizes below one 32-position tile: every chunk is a
+    partial tile (masked), and a row merges up to 200 slots. B = 2 ragged
+    sequences (200 and 37 positions) against the oracle."""
+    cfg = MLAConfig.deepseek_v2()
+    lens = [200, 37]
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    kv = make_cache((int(offs[-1]),), cfg, "bf16", 46, cuda)
+    W_UK, W_UV = make_weights(cfg, "bf16", 47, cuda)
+    q_nope, q_rope = make_queries((len(lens),), cfg, 48, cuda)
+    cos, sin = rope(max(lens), cfg, cuda)
+    ref = oracle_decode(kv, offs, q_nope, q_rope, W_UK, W_UV, cos, sin, cfg)
+    off_t = torch.tensor(offs, dtype=torch.int32, device=cuda)
+    out = F.mla_decode(kv, q_nope, q_rope, W_UK, W_UV, cos, sin, cfg, seq_offsets=off_t, chunk_rows=chunk_rows,
+                       kernel_variant=variant)
+    assert_close(out.cpu().numpy(), ref, "bf16", f"chunk_rows={chunk_rows} variant={variant}")
+
+
+@pytest.mark.parametrize("kv_dtype,w_dtype", [("bf16", "f16"), ("f16", "bf16")])
+def test_mixed_cache_and_weight_dtypes(cuda, kv_dtype, w_dtype):
+    """Cache and weights in different 16-bit types: the attention kernel's
+    queries follow the cache type, the absorb and W_UV projection follow the
+    weights' type."""
+    cfg = MLAConfig.deepseek_v2()
+    B, S = 3, 700
+    kv = make_cache((B, S), cfg, kv_dtype, 56, cuda)
+    W_UK, W_UV = make_weights(cfg, w_dtype, 57, cuda)
+    q_nope, q_rope = make_queries((B,), cfg, 58, cuda)
+    cos, sin = rope(S, cfg, cuda)
+    ref = oracle_decode(kv.reshape(B * S, -1), [b * S for b in range(B + 1)], q_nope, q_rope, W_UK, W_UV, cos, sin,
+                        cfg)
+    out = F.mla_decode(kv, q_nope, q_rope, W_UK, W_UV, cos, sin, cfg)
+    assert_close(out.cpu().numpy(), ref, "bf16", f"cache {kv_dtype}, weights {w_dtype}")
