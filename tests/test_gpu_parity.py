@@ -277,10 +277,13 @@ def test_extension_checks_on_device(cuda):
 
 # ---------------------------------------------------------------------------
 # C ABI: several query tokens per sequence, head counts that leave padded rows
-# in the 32-row query blocks, absorption inside the call, ragged caches
+# in the 32-row query blocks, absorption inside the call, ragged caches; 20
+# heads (query heads not a multiple of 16) take the VALU decode and the MFMA
+# projection of its fp32 partials under the automatic plan
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("heads,qps,variant", [(48, 1, 2), (48, 3, 2), (16, 2, 2), (128, 2, 2), (48, 3, 1)])
+@pytest.mark.parametrize("heads,qps,variant", [(48, 1, 2), (48, 3, 2), (16, 2, 2), (128, 2, 2), (48, 3, 1),
+                                                (20, 1, 0), (20, 3, 0)])
 def test_capi_multi_query_absorb(cuda, heads, qps, variant):
     import ctypes
 
