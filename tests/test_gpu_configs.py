@@ -149,6 +149,49 @@ def test_config2_plan_keeps_partials_below_cache(cuda, abi):
     assert lib.la_mla_decode_workspace_size(ctypes.byref(a)) > cache_bytes
 
 
+def _plan_workspace(B, total, Hq, ncu, chunk_rows=0):
+    """Workspace of the MFMA split plan (q_nope absorbed into 16-bit queries):
+    about one workgroup per CU, chunks of at least ceil(Hq*512/576) rows
+    rounded up to 64; slots = chunks + sequences - 1; regions 256-B aligned:
+    [q_prep (B, Hq padded to 32, 576) 16-bit] [partials (slots*Hq, 512) fp16]
+    [scales (2) and maxima (1) fp32 per partial row] [log-sum-exps fp32]."""
+    def al(x):
+        return (x + 255) // 256 * 256
+
+    if chunk_rows:
+        L = chunk_rows
+    else:
+        chunks = max(1, ncu // ((Hq + 127) // 128))
+        L = -(-total // chunks)
+        L = max(L, -(-(Hq * 512) // 576))
+        L = max(-(-L // 64) * 64, 64)
+    n = -(-total // L)
+    slots = n + B - 1
+    q_prep = al(B * (-(-Hq // 32) * 32) * 576 * 2)
+    return q_prep + al(slots * Hq * 512 * 2) + al(slots * Hq * 3 * 4) + al(slots * Hq * 4), L, n
+
+
+@pytest.mark.parametrize("name", ["cfg2", "cfg3", "cfg4", "cfg5"])
+def test_mfma_plan_at_the_benchmark_configs(cuda, abi, name):
+    """The split plan on the benchmark configurations, pinned by its workspace:
+    one workgroup per CU where the rows allow (config 3: 256 chunks of 1,024
+    rows, config 5: 256 of 2,048, config 4: 253 chunks over the ragged rows),
+    and at B = 1 the 128-row floor that keeps the partial rows below the
+    cache bytes (64 chunks)."""
+    lib, capi = abi
+    inp = bench.build_inputs(name, cuda)
+    cfg = inp["cfg"]
+    out = torch.empty(inp["B"], cfg.num_heads, cfg.v_head_dim, device=cuda)
+    a = bench.decode_args(inp, out, capi)
+    ncu = torch.cuda.get_device_properties(cuda).multi_processor_count
+    want, L, n = _plan_workspace(inp["B"], int(inp["total"]), cfg.num_heads, ncu)
+    got = lib.la_mla_decode_workspace_size(ctypes.byref(a))
+    print(f"[plan {name}] {ncu} CUs: {n} chunks of {L} rows, workspace {got} B", flush=True)
+    assert got == want
+    if name in ("cfg3", "cfg5"):
+        assert n == ncu
+
+
 def test_config3_batched_uniform(cuda, abi):
     lib, capi = abi
     inp = bench.build_inputs("cfg3", cuda)
