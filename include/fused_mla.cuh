@@ -15,7 +15,7 @@
 // return (src/fused_mla.cu:295).
 #pragma once
 
-#include "mla_config.hpp"
+#include "mla_config.cuh"
 
 struct FusedMLAParams {
   const __half* kv_cache;   // (seq_len, kv_lora_rank + qk_rope_head_dim); see kv_dtype

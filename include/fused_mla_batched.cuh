@@ -1,11 +1,11 @@
 // Drop-in for the reference's src/fused_mla_batched.cuh (paths relative to
 // the reference repo): BatchedFusedMLAParams (:7-30) and
 // launch_batched_fused_mla (:35) in the global namespace with HIP types, over
-// the C ABI of latent_attn.h. Same conventions as fused_mla.hpp: reference
+// the C ABI of latent_attn.h. Same conventions as fused_mla.cuh: reference
 // fields in reference order, then defaulted dtype / workspace extensions.
 #pragma once
 
-#include "fused_mla.hpp"
+#include "fused_mla.cuh"
 
 struct BatchedFusedMLAParams {
   const __half* kv_cache;   // shared cache (seq_len, kv_lora_rank + qk_rope_head_dim)

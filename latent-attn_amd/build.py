@@ -7,7 +7,7 @@
   the C ABI; host-only C++ compiled with g++ against torch's headers and
   linked to the library with an $ORIGIN rpath.
 * ``tests/cpp/reference_caller`` -- the C++ drop-in test program (a caller
-  of include/fused_mla.hpp written like the reference's C++ test), run by
+  of include/fused_mla.cuh written like the reference's C++ test), run by
   tests/test_gpu_cpp_caller.py.
 
 Usage: ``python latent-attn_amd/build.py [--lib-only]``. Always recompiles.

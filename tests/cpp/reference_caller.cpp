@@ -21,9 +21,9 @@
 #include <string>
 #include <vector>
 
-#include "fused_mla.hpp"
-#include "fused_mla_batched.hpp"
-#include "mla_config.hpp"
+#include "fused_mla.cuh"
+#include "fused_mla_batched.cuh"
+#include "mla_config.cuh"
 
 #define HIP_CHECK(x)                                                                     \
   do {                                                                                   \

@@ -243,7 +243,8 @@ def test_functional_signatures_match_reference():
 
 
 def test_cpp_dropin_header_compiles_and_links(tmp_path):
-    """include/latent_attn.hpp: reference-style aggregate initialisation of
+    """include/{mla_config,fused_mla,fused_mla_batched}.cuh under the
+    reference's own header names: reference-style aggregate initialisation of
     FusedMLAParams / BatchedFusedMLAParams (src/fused_mla.cuh:11-34,
     src/fused_mla_batched.cuh:7-30) compiles with HIP types and links against
     the library; the workspace query runs on the host."""
@@ -257,16 +258,16 @@ def test_cpp_dropin_header_compiles_and_links(tmp_path):
         pytest.skip("g++ or HIP headers not available")
     src = tmp_path / "dropin.cpp"
     src.write_text(
-        '#include "latent_attn.hpp"\n'
+        '#include "fused_mla.cuh"\n'
+        '#include "fused_mla_batched.cuh"\n'
+        '#include "mla_config.cuh"\n'
         "int main() {\n"
-        "  latent_attn::MLAConfig cfg = latent_attn::MLAConfig::deepseek_v2();\n"
+        "  MLAConfig cfg = MLAConfig::deepseek_v2();\n"
         "  cfg.validate();\n"
-        "  latent_attn::FusedMLAParams p{nullptr, 16, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, &cfg};\n"
-        "  latent_attn::BatchedFusedMLAParams b{nullptr, 16, 2, nullptr, nullptr, nullptr, nullptr, nullptr,\n"
-        "                                      nullptr, &cfg};\n"
+        "  FusedMLAParams p{nullptr, 16, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, &cfg};\n"
+        "  BatchedFusedMLAParams b{nullptr, 16, 2, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, &cfg};\n"
         "  if (p.kv_dtype != LA_DTYPE_F16 || b.batch_size != 2) return 2;\n"
-        "  if (latent_attn::launch_fused_mla(latent_attn::FusedMLAParams{}) != hipErrorInvalidValue) return 3;\n"
-        "  // the reference's names without a qualifier (src/fused_mla.cuh, src/mla_config.cuh)\n"
+        "  if (launch_fused_mla(FusedMLAParams{}) != hipErrorInvalidValue) return 3;\n"
         "  MLAConfig c2 = MLAConfig::deepseek_v3();\n"
         "  FusedMLAParams q; q.cfg = nullptr;\n"
         "  if (launch_fused_mla(q) != hipErrorInvalidValue) return 4;\n"
@@ -278,7 +279,7 @@ def test_cpp_dropin_header_compiles_and_links(tmp_path):
         "  const la_mla_config cc = c2.c_abi();\n"
         "  if (fused_mla_workspace_size(16, 2, c2, LA_DTYPE_BF16, LA_DTYPE_BF16) >\n"
         "      la_fused_mla_workspace_size(16, 2, &cc)) return 6;\n"
-        "  return latent_attn::fused_mla_workspace_size(16, 2, cfg) > 0 ? 0 : 1;\n"
+        "  return fused_mla_workspace_size(16, 2, cfg) > 0 ? 0 : 1;\n"
         "}\n")
     libdir = os.path.join(REPO, "latent-attn_amd", "latent_attn")
     exe = tmp_path / "dropin"

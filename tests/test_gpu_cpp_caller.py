@@ -1,5 +1,5 @@
-"""GPU run of a C++ caller of the drop-in headers (include/fused_mla.hpp,
-fused_mla_batched.hpp, mla_config.hpp), checked against the float64 oracle.
+"""GPU run of a C++ caller of the drop-in headers (include/fused_mla.cuh,
+fused_mla_batched.cuh, mla_config.cuh, included by the reference's own file names), checked against the float64 oracle.
 
 tests/cpp/reference_caller.cpp is written the way the reference's C++ test
 is (reference tests/test_correctness.cu): srand(42) uniform inputs of small
