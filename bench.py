@@ -301,6 +301,123 @@ def time_fp8(lib, hip, capi, inp, out, stream, steps: int = 100) -> dict:
             "attn_frac_of_8TBps": round(fp8_bytes / (kern_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
+def time_fp16(lib, hip, capi, inp, out, stream, steps: int = 100) -> dict:
+    """The same decode step with the reference's contract dtype: an fp16 copy
+    of the cache and fp16 W_UK / W_UV (the reference binding accepts float16
+    only, csrc/bindings.cpp:28-33), timed like the fp8 leg."""
+    import torch
+
+    kv16 = inp["kv"].to(torch.float16)
+    wuk16, wuv16 = inp["W_UK"].to(torch.float16), inp["W_UV"].to(torch.float16)
+    a = decode_args(inp, out, capi)
+    a.kv_cache, a.kv_dtype = kv16.data_ptr(), capi.LA_DTYPE_F16
+    a.W_UK, a.w_uk_dtype = wuk16.data_ptr(), capi.LA_DTYPE_F16
+    a.W_UV, a.w_uv_dtype = wuv16.data_ptr(), capi.LA_DTYPE_F16
+    need = lib.la_mla_decode_workspace_size(ctypes.byref(a))
+    ws16 = torch.empty(need, dtype=torch.uint8, device=kv16.device)
+    a.workspace, a.workspace_bytes = ws16.data_ptr(), need
+
+    def step(ev_b=None, ev_e=None, repeat=0):
+        decode_call(lib, a, stream, ev_b, ev_e, repeat, " (fp16)")
+
+    for _ in range(20):
+        step()
+    settle_clocks(step, 50)
+    us = time_steps(hip, step, stream, steps) * 1e3
+    kern = time_attention(hip, step)
+    kern_us = sum(kern) / len(kern) * 1e3
+    cache_bytes = int(inp["total"]) * BYTES_PER_POS
+    return {"step_us": round(us, 2), "attn_kernel_us": round(kern_us, 2),
+            "attn_frac_of_8TBps": round(cache_bytes / (kern_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def reference_entry_legs(lib, capi, hip, dev, stream) -> dict:
+    """The reference's own launch entry points over the reference's own
+    benchmark matrix, fp16 cache and weights (its contract dtype), DeepSeek-V2
+    dims (DeepSeek-V3 has the same attention shapes: only d_model differs),
+    pre-absorbed fp32 queries:
+      * la_fused_mla (launch_fused_mla): one query token at kv_len 512, 2048,
+        8192 and 32768 (reference benchmarks/bench_latency.cu:252-271);
+      * la_batched_fused_mla (launch_batched_fused_mla): B query tokens over
+        one shared cache, B in {1, 4, 16, 64} x kv_len {2048, 8192}
+        (reference benchmarks/bench_throughput.py:86-93).
+    Each entry: microseconds per call (50 calls back to back on the GPU, a
+    spin kernel holding the stream while the host enqueues them, after 10
+    untimed calls), tokens/s, and the attention kernel's time (the same
+    arguments through la_mla_decode_profiled, 10 x 10 back-to-back launches)
+    with its fraction of 8 TB/s on the cache bytes read once (kv_len x 1152 B;
+    a shared cache is read by every 128-head group, the extra reads hit L2)."""
+    import torch
+
+    from latent_attn import MLAConfig, build_rope_tables
+
+    cfg = MLAConfig.deepseek_v2()
+    row = cfg.kv_lora_rank + cfg.qk_rope_head_dim
+    g = torch.Generator(device=dev).manual_seed(3)
+    std = 1.0 / math.sqrt(cfg.kv_lora_rank)
+    W_UV = (torch.randn(cfg.num_heads * cfg.v_head_dim, cfg.kv_lora_rank, generator=g, device=dev) * std).half()
+    c_cfg = capi.config(cfg)
+
+    def leg(entry: str, S: int, B: int) -> dict:
+        kv = torch.randn(S, row, generator=g, device=dev).half()
+        qa = torch.randn(B, cfg.num_heads, cfg.kv_lora_rank, generator=g, device=dev) * std
+        qr = torch.randn(B, cfg.num_heads, cfg.qk_rope_head_dim, generator=g, device=dev)
+        cos, sin = build_rope_tables(S, cfg.qk_rope_head_dim, device=dev)
+        cos, sin = cos.contiguous(), sin.contiguous()
+        out = torch.empty(B, cfg.num_heads, cfg.v_head_dim, device=dev)
+        need = lib.la_fused_mla_workspace_size_dt(S, B, ctypes.byref(c_cfg), capi.LA_DTYPE_F16, capi.LA_DTYPE_F16)
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+        vp = ctypes.c_void_p
+
+        def call():
+            if entry == "la_fused_mla":
+                st = lib.la_fused_mla(vp(kv.data_ptr()), capi.LA_DTYPE_F16, S, vp(qa.data_ptr()), vp(qr.data_ptr()),
+                                      vp(W_UV.data_ptr()), capi.LA_DTYPE_F16, vp(cos.data_ptr()), vp(sin.data_ptr()),
+                                      vp(out.data_ptr()), ctypes.byref(c_cfg), vp(ws.data_ptr()), need, vp(stream))
+            else:
+                st = lib.la_batched_fused_mla(vp(kv.data_ptr()), capi.LA_DTYPE_F16, S, B, vp(qa.data_ptr()),
+                                              vp(qr.data_ptr()), vp(W_UV.data_ptr()), capi.LA_DTYPE_F16,
+                                              vp(cos.data_ptr()), vp(sin.data_ptr()), vp(out.data_ptr()),
+                                              ctypes.byref(c_cfg), vp(ws.data_ptr()), need, vp(stream))
+            if st != 0:
+                raise RuntimeError(f"{entry}: {lib.la_status_string(st).decode()}")
+
+        for _ in range(10):
+            call()
+        t0, t1 = new_event(hip), new_event(hip)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(8_000_000)
+        hip.hipEventRecord(t0, ctypes.c_void_p(stream))
+        for _ in range(50):
+            call()
+        hip.hipEventRecord(t1, ctypes.c_void_p(stream))
+        hip.hipEventSynchronize(t1)
+        us = elapsed_ms(hip, t0, t1) * 1e3 / 50
+        hip.hipEventDestroy(t0)
+        hip.hipEventDestroy(t1)
+        # the same arguments as the entry point builds them (one shared cache,
+        # B query tokens per sequence), for the attention kernel's own time
+        a = capi.DecodeArgs()
+        a.kv_cache, a.kv_dtype, a.total_rows = kv.data_ptr(), capi.LA_DTYPE_F16, S
+        a.num_seqs, a.seq_len, a.queries_per_seq = 1, S, B
+        a.q_absorbed, a.q_rope = qa.data_ptr(), qr.data_ptr()
+        a.W_UV, a.w_uv_dtype = W_UV.data_ptr(), capi.LA_DTYPE_F16
+        a.rope_cos, a.rope_sin, a.rope_rows = cos.data_ptr(), sin.data_ptr(), S
+        a.output, a.cfg = out.data_ptr(), c_cfg
+        a.workspace, a.workspace_bytes = ws.data_ptr(), need
+        kern = time_attention(hip, lambda b=None, e=None, r=0: decode_call(lib, a, stream, b, e, r, f" ({entry})"))
+        kern_us = sum(kern) / len(kern) * 1e3
+        return {"kv_len": S, "batch": B, "us_per_call": round(us, 2), "tokens_per_s": round(B / (us * 1e-6), 1),
+                "attn_kernel_us": round(kern_us, 2),
+                "attn_frac_of_8TBps": round(S * BYTES_PER_POS / (kern_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+    res = {"dtype": "fp16 cache and weights, fp32 queries", "model": "DeepSeek-V2 dims (128 heads, 512 + 64)",
+           "la_fused_mla": [leg("la_fused_mla", S, 1) for S in (512, 2048, 8192, 32768)],
+           "la_batched_fused_mla": [leg("la_batched_fused_mla", S, B) for B in (1, 4, 16, 64) for S in (2048, 8192)]}
+    torch.cuda.empty_cache()
+    return res
+
+
 def time_layer(hip, inp, stream, calls: int = 20) -> dict:
     """LatentAttentionLayer.forward_batch (DeepSeek-V2 dims, fp32 parameters
     as in the reference module) for one token per sequence over the
@@ -347,26 +464,38 @@ def measured_traffic(config: str):
         return None
 
 
-def cpu_baseline(inp, budget_s: float = 10.0):
-    """CPU baseline on the box's host cores, two restatements of the
-    reference path from oracle/mla_oracle.py in float32, each on whole
-    sequences of the workload one at a time until ~budget_s, extrapolated by
-    positions to one step (all B sequences):
-      * value: the decompress-then-attend math of the reference's PyTorch
-        path (tests/test_python.py:26-63, oracle naive_mla): K_nope = c_t
-        W_UK^T and V = c_t W_UV^T materialised per sequence;
-      * absorbed: the reference kernel's algorithm (src/fused_mla.cu:218-267,
-        oracle absorb_q + absorbed_latent + project_wuv)."""
-    import numpy as np
-
-    from oracle import mla_oracle as mo
-
+def host_info() -> dict:
+    """The host's logical CPU count, CPU model and numpy's thread-pool size."""
     try:
         from threadpoolctl import threadpool_info
 
         threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
     except Exception:  # pragma: no cover
         threads = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"os_cpu_count": os.cpu_count(), "cpu_model": model, "numpy_threads": int(threads)}
+
+
+def cpu_time_path(inp, kind: str, budget_s: float, max_pos: int = 0):
+    """Seconds of the oracle's float32 `kind` path ("naive": the reference's
+    PyTorch decompress-then-attend math, tests/test_python.py:26-63, oracle
+    naive_mla; "absorbed": the reference kernel's algorithm,
+    src/fused_mla.cu:218-267, oracle absorb_q + absorbed_latent +
+    project_wuv) on the workload's sequences one at a time until budget_s,
+    each cut to its first max_pos positions when max_pos > 0. Returns
+    (seconds, sequences, positions)."""
+    import numpy as np
+
+    from oracle import mla_oracle as mo
+
     cfg = inp["cfg"]
     d = mo.Dims(cfg.d_model, cfg.kv_lora_rank, cfg.qk_nope_head_dim, cfg.qk_rope_head_dim, cfg.num_heads,
                 cfg.v_head_dim)
@@ -376,40 +505,72 @@ def cpu_baseline(inp, budget_s: float = 10.0):
     sin = inp["sin"].cpu().numpy()
     lens = [int(x) for x in inp["lens"]]
     offs = np.concatenate([[0], np.cumsum(lens)])
-    total_pos = int(sum(lens))
+    done_pos, done_seq, spent = 0, 0, 0.0
+    while spent < budget_s and done_seq < inp["B"]:
+        b = done_seq
+        n = lens[b] if max_pos <= 0 else min(lens[b], max_pos)
+        kv = inp["kv"][offs[b]:offs[b] + n].float().cpu().numpy()
+        qn = inp["q_nope"][b].cpu().numpy()
+        qr = inp["q_rope"][b].cpu().numpy()
+        t0 = time.perf_counter()
+        if kind == "naive":
+            mo.naive_mla(kv, W_UK, W_UV, qn, qr, cos, sin, d, dtype=np.float32)
+        else:
+            qa = mo.absorb_q(qn, W_UK, d, dtype=np.float32)
+            acc, _ = mo.absorbed_latent(kv, qa, qr, cos, sin, d, dtype=np.float32)
+            mo.project_wuv(acc, W_UV, d, dtype=np.float32)
+        spent += time.perf_counter() - t0
+        done_pos += n
+        done_seq += 1
+    return spent, done_seq, done_pos
 
-    def run(kind):
-        done_pos, done_seq, spent = 0, 0, 0.0
-        while spent < budget_s and done_seq < inp["B"]:
-            b = done_seq
-            kv = inp["kv"][offs[b]:offs[b + 1]].float().cpu().numpy()
-            qn = inp["q_nope"][b].cpu().numpy()
-            qr = inp["q_rope"][b].cpu().numpy()
-            t0 = time.perf_counter()
-            if kind == "naive":
-                mo.naive_mla(kv, W_UK, W_UV, qn, qr, cos, sin, d, dtype=np.float32)
-            else:
-                qa = mo.absorb_q(qn, W_UK, d, dtype=np.float32)
-                acc, _ = mo.absorbed_latent(kv, qa, qr, cos, sin, d, dtype=np.float32)
-                mo.project_wuv(acc, W_UV, d, dtype=np.float32)
-            spent += time.perf_counter() - t0
-            done_pos += lens[b]
-            done_seq += 1
-        return spent / done_pos * total_pos * 1e6, done_seq, done_pos
 
-    naive_us, n_seq, n_pos = run("naive")
-    abs_us, a_seq, a_pos = run("absorbed")
+def cpu_baseline(inp, budget_s: float = 10.0):
+    """CPU baseline on the box's host cores: the oracle's float32 naive and
+    absorbed paths (cpu_time_path) on whole sequences of the workload until
+    ~budget_s each, extrapolated by positions to one step (all B sequences)."""
+    total_pos = int(sum(int(x) for x in inp["lens"]))
+    host = host_info()
+    n_s, n_seq, n_pos = cpu_time_path(inp, "naive", budget_s)
+    a_s, a_seq, a_pos = cpu_time_path(inp, "absorbed", budget_s)
     return {
-        "value": round(naive_us, 1),
+        "value": round(n_s / n_pos * total_pos * 1e6, 1),
         "unit": "us/step",
-        "cores": int(threads),
+        "cores": host["numpy_threads"],
         "kind": "port",
         "sample": f"{n_seq} of {inp['B']} sequences ({n_pos} positions) through oracle/mla_oracle.py naive_mla "
                   f"(the reference's PyTorch decompress-then-attend math) in float32, extrapolated by positions",
-        "absorbed": {"value": round(abs_us, 1), "unit": "us/step",
+        "host": host,
+        "absorbed": {"value": round(a_s / a_pos * total_pos * 1e6, 1), "unit": "us/step",
                      "sample": f"{a_seq} of {inp['B']} sequences ({a_pos} positions) through the absorbed "
                                f"float32 path (absorb_q, absorbed_latent, project_wuv)"},
     }
+
+
+def cpu_baseline_configs(dev, budget_s: float = 4.0) -> dict:
+    """The CPU paths on the other configurations (same seeded inputs as their
+    GPU legs, same host threads): the absorbed float32 path on configs 2, 4
+    and 5, the naive float32 path on config 2 and on the first 4,096
+    positions of config 5's first sequence, each extrapolated by positions to
+    one step of its configuration."""
+    import torch
+
+    res = {}
+    for name, kinds in (("cfg2", ("absorbed", "naive")), ("cfg4", ("absorbed",)), ("cfg5", ("absorbed", "naive"))):
+        inp = build_inputs(name, dev)
+        total_pos = int(sum(int(x) for x in inp["lens"]))
+        leg = {}
+        for kind in kinds:
+            cut = 4096 if (name == "cfg5" and kind == "naive") else 0
+            sec, nseq, npos = cpu_time_path(inp, kind, budget_s, cut)
+            key = kind if not cut else "naive_slice_4096"
+            leg[key] = {"us_per_step": round(sec / npos * total_pos * 1e6, 1),
+                        "sample": f"{nseq} sequence(s), {npos} positions" + (
+                            f" (the first {cut} of a {int(inp['lens'][0])}-position sequence)" if cut else "")}
+        res[name] = leg
+        del inp
+        torch.cuda.empty_cache()
+    return res
 
 
 class Stepper:
@@ -485,6 +646,35 @@ def time_attention(hip, step, calls: int = 10, repeat: int = 10) -> list:
         hip.hipEventDestroy(b)
         hip.hipEventDestroy(e)
     return ms
+
+
+def time_ceiling(lib, hip, a, stream, cache_bytes: int, calls: int = 10, repeat: int = 10) -> dict:
+    """Streaming ceiling of the attention kernel's copy schedule
+    (la_stream_ceiling): its grid and every wave's HBM->LDS copies per tile,
+    no compute, into a ring of 3 tile buffers (the kernel's: one tile in
+    flight at its end-of-iteration wait) or 4 (the deepest 160 KB of LDS
+    holds). Microseconds per launch over `calls` x `repeat` back-to-back
+    launches between fence-free event pairs, and the cache rate."""
+    import torch
+
+    res = {}
+    for ring in (3, 4):
+        for _ in range(3):
+            st = lib.la_stream_ceiling(ctypes.byref(a), ring, ctypes.c_void_p(stream), None, None, 1)
+            if st != 0:
+                raise RuntimeError(f"la_stream_ceiling: {lib.la_status_string(st).decode()}")
+        evs = [(new_event(hip, True), new_event(hip, True)) for _ in range(calls)]
+        for b, e in evs:
+            assert lib.la_stream_ceiling(ctypes.byref(a), ring, ctypes.c_void_p(stream), b, e, repeat) == 0
+        torch.cuda.synchronize()
+        us = sum(elapsed_ms(hip, b, e) / repeat for b, e in evs) / calls * 1e3
+        for b, e in evs:
+            hip.hipEventDestroy(b)
+            hip.hipEventDestroy(e)
+        gbps = cache_bytes / (us * 1e-6) / 1e9
+        res[f"ring{ring}"] = {"us": round(us, 2), "cache_GBps": round(gbps, 1),
+                              "frac_of_8TBps": round(gbps / HBM_PEAK_GBPS, 4)}
+    return res
 
 
 def time_mall_cold(hip, step, stream, dev, steps: int = 30, flush_mib: int = 1024) -> dict:
@@ -584,6 +774,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fp8", action="store_true",
                     help="skip the leg over an FP8 E4M3 copy of the cache")
+    ap.add_argument("--no-fp16", action="store_true",
+                    help="skip the leg over an fp16 copy of the cache and weights (the reference's dtype)")
+    ap.add_argument("--no-reference-legs", action="store_true",
+                    help="skip la_fused_mla / la_batched_fused_mla over the reference's benchmark matrix")
     ap.add_argument("--layer", action="store_true",
                     help="also time LatentAttentionLayer.forward_batch (fp32 projections, 1.8 GB of weights) "
                          "on the same batch and cache")
@@ -635,11 +829,14 @@ def main():
     kern_ms = time_attention(hip, step)
     kern_avg = sum(kern_ms) / len(kern_ms)
     us_step = ms_step * 1e3
+    log("[bench] streaming ceiling of the copy schedule")
+    ceiling = time_ceiling(lib, hip, step.a, stream, int(inp["total"]) * BYTES_PER_POS) if inp["offsets"] is None else None
     log("[bench] append / paged legs")
     append_us = time_append(lib, hip, capi, inp, stream)
     paged = time_paged(lib, hip, capi, inp, step.out, step.ws, stream) if inp["offsets"] is None else None
     layer = time_layer(hip, inp, stream) if args.layer else None
     fp8 = time_fp8(lib, hip, capi, inp, step.out, stream) if not args.no_fp8 and inp["offsets"] is None else None
+    fp16 = time_fp16(lib, hip, capi, inp, step.out, stream) if not args.no_fp16 else None
     mall = None
     if not args.no_mall_cold:
         log("[bench] MALL-cold leg")
@@ -686,6 +883,8 @@ def main():
         **({"mall_cold": mall} if mall else {}),
         **({"layer_forward_batch": layer} if layer else {}),
         **({"fp8_cache": fp8} if fp8 else {}),
+        **({"fp16_cache": fp16} if fp16 else {}),
+        **({"stream_ceiling": ceiling} if ceiling else {}),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved_gbps, 1),
@@ -704,9 +903,15 @@ def main():
             log(f"[bench] leg {c}")
             line["other_configs"][c] = config_leg(lib, capi, hip, c, device, stream)
         inp = build_inputs(args.config, device) if not args.no_cpu_baseline else None
+    if not args.no_reference_legs:
+        log("[bench] reference entry points (la_fused_mla, la_batched_fused_mla)")
+        line["reference_entry_points"] = reference_entry_legs(lib, capi, hip, device, stream)
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
         line["cpu_baseline"] = cpu_baseline(inp)
+        if legs:
+            log("[bench] cpu baseline, other configurations")
+            line["cpu_baseline"]["other_configs"] = cpu_baseline_configs(device)
     print(json.dumps(line), flush=True)
 
 

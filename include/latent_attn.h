@@ -221,6 +221,36 @@ size_t la_mla_decode_workspace_size(const la_decode_args* args);
  * combine -> W_UV projection. */
 int la_mla_decode(const la_decode_args* args, void* stream);
 
+/* The plan la_mla_decode would run for `args` on the current device. No
+ * counterpart in the reference (its launch has no split plan); for callers
+ * that size or schedule around the step and for tests. */
+enum {
+  LA_PLAN_ATTENTION_VALU = 1, /* decode_generic_kernel (any dtype and head shape) */
+  LA_PLAN_ATTENTION_MFMA = 2  /* decode_mfma_kernel (kv_lora_rank 512, rope 64, 16-bit or FP8 cache, gfx950) */
+};
+enum {
+  LA_PLAN_MERGE_VALU = 1,        /* combine_project_kernel */
+  LA_PLAN_MERGE_MFMA = 2,        /* merge_project_kernel: full partial rows per workgroup */
+  LA_PLAN_MERGE_MFMA_HALVES = 3  /* merge_project_half_kernel: latent halves added into the output */
+};
+enum {
+  LA_PLAN_ABSORB_NONE = 0,       /* queries come absorbed (q_absorbed) */
+  LA_PLAN_ABSORB_VALU = 1,       /* absorb_kernel into fp32 q_abs */
+  LA_PLAN_ABSORB_MFMA = 2,       /* absorb_mfma_kernel into fp32 q_abs */
+  LA_PLAN_ABSORB_MFMA_QPREP = 3  /* absorb_mfma_kernel straight into the attention kernel's 16-bit queries */
+};
+typedef struct la_plan_info {
+  int32_t attention;   /* LA_PLAN_ATTENTION_* (0 when num_seqs == 0) */
+  int32_t chunk_rows;  /* rows per split-KV chunk */
+  int32_t num_chunks;
+  int32_t num_slots;   /* partial slots per query head: num_chunks + num_seqs - 1 */
+  int32_t head_groups; /* query-head groups per chunk (workgroups = num_chunks x head_groups, rounded for the XCDs) */
+  int32_t merge;       /* LA_PLAN_MERGE_* */
+  int32_t absorb;      /* LA_PLAN_ABSORB_* */
+  size_t workspace_bytes; /* la_mla_decode_workspace_size(args) */
+} la_plan_info;
+int la_mla_decode_plan(const la_decode_args* args, la_plan_info* info);
+
 /* la_mla_decode for profilers and benchmarks that time the split-KV attention
  * kernel alone. No counterpart in the reference. event_begin / event_end:
  * optional hipEvent_t handles recorded on `stream` right before and right
@@ -231,6 +261,21 @@ int la_mla_decode(const la_decode_args* args, void* stream);
  * once; negative = LA_ERROR_INVALID_VALUE. */
 int la_mla_decode_profiled(const la_decode_args* args, void* stream, void* event_begin, void* event_end,
                            int32_t repeat);
+
+/* Streaming-ceiling measurement of the attention kernel's copy schedule. No
+ * counterpart in the reference; for benchmarks and profilers. Runs, with the
+ * plan la_mla_decode would use for `args`, a copies-only variant of the MFMA
+ * attention kernel: the same grid and block mapping and, per 32-position
+ * tile, the same HBM->LDS copies of every wave (cache rows, k_rope rows,
+ * RoPE table rows) into a ring of `ring` tile buffers (3: the kernel's own
+ * ring; 4: the deepest one 160 KB of LDS holds), with one barrier per tile
+ * and no compute. It reads the cache and the tables and writes nothing to
+ * device memory (the output and workspace are untouched). repeat and the
+ * optional events behave as in la_mla_decode_profiled. Returns
+ * LA_ERROR_NOT_SUPPORTED unless args select the MFMA kernel on a contiguous
+ * BF16 / F16 cache. */
+int la_stream_ceiling(const la_decode_args* args, int32_t ring, void* stream, void* event_begin, void* event_end,
+                      int32_t repeat);
 
 /* la_mla_decode without any allocation. No counterpart in the reference: for
  * callers that cannot allocate device memory (code under HIP graph capture,

@@ -40,8 +40,17 @@ int dtype_tag(const torch::Tensor& t) {
   }
 }
 
+// Caches (and the rows appended to them) may be FP8 E4M3 besides the 16- and
+// 32-bit types; weights may not (check_weight).
 void check_storage(const torch::Tensor& t, const char* name) {
-  TORCH_CHECK(dtype_tag(t) >= 0, name, " must be float16, bfloat16 or float32, got ", t.dtype());
+  TORCH_CHECK(dtype_tag(t) >= 0, name, " must be float16, bfloat16, float32 or float8_e4m3fn, got ", t.dtype());
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+  TORCH_CHECK(t.is_cuda(), name, " must be on CUDA");
+}
+
+void check_weight(const torch::Tensor& t, const char* name) {
+  TORCH_CHECK(dtype_tag(t) >= 0 && dtype_tag(t) != LA_DTYPE_FP8_E4M3, name,
+              " must be float16, bfloat16 or float32, got ", t.dtype());
   TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
   TORCH_CHECK(t.is_cuda(), name, " must be on CUDA");
 }
@@ -88,7 +97,7 @@ torch::Tensor fused_mla_forward(torch::Tensor kv_cache, torch::Tensor q_absorbed
   check_storage(kv_cache, "kv_cache");
   check_fp32_contiguous(q_absorbed, "q_absorbed");
   check_fp32_contiguous(q_rope, "q_rope");
-  check_storage(W_UV, "W_UV");
+  check_weight(W_UV, "W_UV");
   check_fp32_contiguous(rope_cos, "rope_cos");
   check_fp32_contiguous(rope_sin, "rope_sin");
   la_mla_config cfg =
@@ -128,7 +137,7 @@ torch::Tensor batched_fused_mla_forward(torch::Tensor kv_cache, torch::Tensor q_
   check_storage(kv_cache, "kv_cache");
   check_fp32_contiguous(q_absorbed, "q_absorbed");
   check_fp32_contiguous(q_rope, "q_rope");
-  check_storage(W_UV, "W_UV");
+  check_weight(W_UV, "W_UV");
   check_fp32_contiguous(rope_cos, "rope_cos");
   check_fp32_contiguous(rope_sin, "rope_sin");
   la_mla_config cfg =
@@ -276,8 +285,8 @@ torch::Tensor mla_decode_forward(torch::Tensor kv_cache, torch::Tensor q_nope, t
   check_storage(kv_cache, "kv_cache");
   check_fp32_contiguous(q_nope, "q_nope");
   check_fp32_contiguous(q_rope, "q_rope");
-  check_storage(W_UK, "W_UK");
-  check_storage(W_UV, "W_UV");
+  check_weight(W_UK, "W_UK");
+  check_weight(W_UV, "W_UV");
   check_fp32_contiguous(rope_cos, "rope_cos");
   check_fp32_contiguous(rope_sin, "rope_sin");
   la_mla_config cfg =
@@ -308,7 +317,7 @@ torch::Tensor mla_decode_absorbed_forward(torch::Tensor kv_cache, torch::Tensor 
   check_storage(kv_cache, "kv_cache");
   check_fp32_contiguous(q_absorbed, "q_absorbed");
   check_fp32_contiguous(q_rope, "q_rope");
-  check_storage(W_UV, "W_UV");
+  check_weight(W_UV, "W_UV");
   check_fp32_contiguous(rope_cos, "rope_cos");
   check_fp32_contiguous(rope_sin, "rope_sin");
   la_mla_config cfg =
@@ -434,7 +443,7 @@ void append_kv_forward(torch::Tensor kv_cache, torch::Tensor seq_lens, torch::Te
 torch::Tensor absorb_q_forward(torch::Tensor q_nope, torch::Tensor W_UK, int d_model, int kv_lora_rank,
                                int qk_nope_head_dim, int qk_rope_head_dim, int num_heads, int v_head_dim) {
   check_fp32_contiguous(q_nope, "q_nope");
-  check_storage(W_UK, "W_UK");
+  check_weight(W_UK, "W_UK");
   la_mla_config cfg =
       config_from_args(d_model, kv_lora_rank, qk_nope_head_dim, qk_rope_head_dim, num_heads, v_head_dim);
   TORCH_CHECK(q_nope.dim() >= 2 && q_nope.size(-1) == qk_nope_head_dim && q_nope.size(-2) == num_heads,
@@ -462,8 +471,8 @@ torch::Tensor naive_mla_forward(torch::Tensor kv_cache, torch::Tensor W_UK, torc
                                 torch::Tensor rope_sin, int d_model, int kv_lora_rank, int qk_nope_head_dim,
                                 int qk_rope_head_dim, int num_heads, int v_head_dim) {
   check_storage(kv_cache, "kv_cache");
-  check_storage(W_UK, "W_UK");
-  check_storage(W_UV, "W_UV");
+  check_weight(W_UK, "W_UK");
+  check_weight(W_UV, "W_UV");
   check_fp32_contiguous(q_nope, "q_nope");
   check_fp32_contiguous(q_rope, "q_rope");
   check_fp32_contiguous(rope_cos, "rope_cos");

@@ -154,12 +154,20 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
     int64_t target_blocks = pl.mfma ? ncu : 4LL * ncu;
     int64_t chunks = std::max<int64_t>(1, target_blocks / std::max<int64_t>(1, groups));
     L = (total + chunks - 1) / chunks;
-    // MFMA path: a chunk writes Hq partial rows of dc fp16 values; keep them
-    // below the chunk's cache bytes (16-bit rows of dc + dR), so short
-    // batches (B = 1) do not trade a cheaper attention launch for a merge
-    // that reads more than the cache (Hq = 128: at least 128 rows).
-    if (pl.mfma) L = std::max<int64_t>(L, ((int64_t)p->Hq * c.kv_lora_rank + c.kv_lora_rank + c.qk_rope_head_dim - 1) /
-                                            (c.kv_lora_rank + c.qk_rope_head_dim));
+    // MFMA path: each workgroup (one chunk, one group of up to 128 query
+    // heads) writes a partial row of dc fp16 values per head; keep them
+    // below the bytes the workgroup streams from a 16-bit cache (rows of
+    // dc + dR), so short batches (B = 1) do not trade a cheaper attention
+    // launch for a merge that reads more than the cache: 128 heads need at
+    // least 114 rows (128 after rounding). The floor counts rows, so for an
+    // FP8 cache (rows of half the bytes) the partials may reach twice the
+    // cache bytes. Head groups share a chunk's rows (several queries over
+    // one cache), each writing its own partials, so the floor is per group.
+    if (pl.mfma) {
+      const int64_t hg = std::min<int64_t>(p->Hq, mfma_heads_per_group());
+      L = std::max<int64_t>(L, (hg * c.kv_lora_rank + c.kv_lora_rank + c.qk_rope_head_dim - 1) /
+                                   (c.kv_lora_rank + c.qk_rope_head_dim));
+    }
     L = (L + 63) / 64 * 64;
     L = std::max<int64_t>(L, 64);
   }
@@ -206,6 +214,16 @@ int prepare(const la_decode_args* a, DecodeProblem* p, Plan* plan) {
   return LA_SUCCESS;
 }
 
+// The latent-half merge: few query rows leave most CUs idle in the full-row
+// merge, so it is split over the two latent halves, which add into the
+// output (zeroed first by the kernel that writes the attention kernel's
+// 16-bit queries: the absorb kernel, or prep_q when the queries come
+// absorbed and there is at least one chunk).
+bool merge_halves(const DecodeProblem& p, const Plan& plan) {
+  return plan.proj_mfma && plan.mfma && (plan.absorb_prep || plan.num_chunks > 0) &&
+         merge_project_blocks(p) < cu_count();
+}
+
 // ev_b / ev_e (optional) are recorded around the attention kernel, which runs
 // max(repeat, 1) times between them.
 int run(const la_decode_args* a, hipStream_t stream, hipEvent_t ev_b = nullptr, hipEvent_t ev_e = nullptr,
@@ -245,8 +263,7 @@ int run(const la_decode_args* a, hipStream_t stream, hipEvent_t ev_b = nullptr, 
   // the two latent halves, which add into the output. The kernel that writes
   // the attention kernel's 16-bit queries (the absorb kernel, or prep_q when
   // the queries come absorbed) runs first and zeroes the output.
-  const bool merge_halves = plan.proj_mfma && plan.mfma && (plan.absorb_prep || plan.num_chunks > 0) &&
-                            merge_project_blocks(p) < cu_count();
+  const bool merge_halves = la::merge_halves(p, plan);
   float* const zero_out = merge_halves ? a->output : nullptr;
   const int64_t zero_n = merge_halves ? tokens * c.num_heads * c.v_head_dim : 0;
   if (a->q_nope) {
@@ -381,12 +398,52 @@ size_t la_mla_decode_workspace_size(const la_decode_args* args) {
   return plan.total;
 }
 
+int la_mla_decode_plan(const la_decode_args* args, la_plan_info* info) {
+  if (!info) return LA_ERROR_INVALID_VALUE;
+  la::DecodeProblem p;
+  la::Plan plan;
+  const int st = la::prepare(args, &p, &plan);
+  if (st != LA_SUCCESS) return st;
+  *info = la_plan_info{};
+  info->workspace_bytes = plan.total;
+  if (args->num_seqs == 0) return LA_SUCCESS;
+  info->attention = plan.mfma ? LA_PLAN_ATTENTION_MFMA : LA_PLAN_ATTENTION_VALU;
+  info->chunk_rows = plan.chunk_len;
+  info->num_chunks = plan.num_chunks;
+  info->num_slots = plan.num_slots;
+  info->head_groups = plan.mfma ? (p.Hq + la::mfma_heads_per_group() - 1) / la::mfma_heads_per_group() : p.Hq;
+  if (!plan.proj_mfma) info->merge = LA_PLAN_MERGE_VALU;
+  else info->merge = la::merge_halves(p, plan) ? LA_PLAN_MERGE_MFMA_HALVES : LA_PLAN_MERGE_MFMA;
+  if (!args->q_nope) info->absorb = LA_PLAN_ABSORB_NONE;
+  else if (plan.absorb_prep) info->absorb = LA_PLAN_ABSORB_MFMA_QPREP;
+  else info->absorb = plan.absorb_mfma ? LA_PLAN_ABSORB_MFMA : LA_PLAN_ABSORB_VALU;
+  return LA_SUCCESS;
+}
+
 int la_mla_decode(const la_decode_args* args, void* stream) { return la::run(args, static_cast<hipStream_t>(stream)); }
 
 int la_mla_decode_profiled(const la_decode_args* args, void* stream, void* event_begin, void* event_end,
                            int32_t repeat) {
   return la::run(args, static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(event_begin),
                  static_cast<hipEvent_t>(event_end), repeat);
+}
+
+int la_stream_ceiling(const la_decode_args* args, int32_t ring, void* stream, void* event_begin, void* event_end,
+                      int32_t repeat) {
+  if (ring != 3 && ring != 4 || repeat < 0) return LA_ERROR_INVALID_VALUE;
+  la::DecodeProblem p;
+  la::Plan plan;
+  const int st = la::prepare(args, &p, &plan);
+  if (st != LA_SUCCESS) return st;
+  if (!plan.mfma || p.block_table || (p.kv_dtype != LA_DTYPE_BF16 && p.kv_dtype != LA_DTYPE_F16))
+    return LA_ERROR_NOT_SUPPORTED;
+  if (plan.num_chunks == 0) return LA_SUCCESS;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipSuccess;
+  if (event_begin) e = hipEventRecord(static_cast<hipEvent_t>(event_begin), s);
+  for (int r = 0; r < (repeat > 1 ? repeat : 1) && e == hipSuccess; ++r) e = la::launch_stream_copies(p, ring, s);
+  if (e == hipSuccess && event_end) e = hipEventRecord(static_cast<hipEvent_t>(event_end), s);
+  return e == hipSuccess ? (int)LA_SUCCESS : la::record_hip(e);
 }
 
 int la_mla_decode_noalloc(const la_decode_args* args, void* stream) {
@@ -401,9 +458,7 @@ int la_mla_decode_noalloc(const la_decode_args* args, void* stream) {
   if (plan.total > 0) {
     const int sp = la::scratch_ptr(&a.workspace);
     if (sp != LA_SUCCESS) return sp;
-  } else {
-    a.workspace = &a;  // never dereferenced: the plan needs no workspace
-  }
+  }  // else: no workspace is needed and none is passed
   return la::run(&a, static_cast<hipStream_t>(stream));
 }
 

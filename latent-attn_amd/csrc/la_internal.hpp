@@ -299,6 +299,10 @@ bool generic_supported(const DecodeProblem& p);
 hipError_t launch_decode_mfma(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_begin = nullptr,
                               hipEvent_t ev_end = nullptr);
 bool mfma_supported(const DecodeProblem& p);
+// The attention kernel's grid and copy schedule with no compute (a
+// streaming-ceiling measurement); ring = 3 or 4 tile buffers. 16-bit
+// contiguous caches.
+hipError_t launch_stream_copies(const DecodeProblem& p, int ring, hipStream_t stream);
 int mfma_heads_per_group();
 int mfma_max_chunk_rows();
 // Fills p.q_prep from p.q_abs and p.q_rope (MFMA path only).

@@ -841,18 +841,24 @@ constexpr bool fp8_half_order_ok() {
 static_assert(fp8_half_order_ok(), "fp8 expansion halves overlap");
 
 // Block id -> (chunk, head group), XCD-aware. Workgroups are dispatched
-// round-robin over the 8 XCDs (id % 8), each with its own L2. XCD x gets the
-// contiguous chunk range [x*per, (x+1)*per): the chunks of one sequence share
-// an L2, so the sequence's Q rows are fetched from HBM once per XCD rather than
-// once per chunk, and every XCD streams one contiguous piece of the cache. The
-// head groups of a chunk are adjacent ids on the same XCD. Ids past the last
-// chunk return at once.
+// round-robin over the 8 XCDs (id % 8), each with its own L2. The work items
+// (chunk, group), chunk-major, are cut into 8 contiguous ranges, one per XCD
+// (XCD x: items [x*per, (x+1)*per), id = 8 k + x is item x*per + k). With
+// one head group per chunk the chunks of one sequence share an L2, so the
+// sequence's Q rows are fetched from HBM once per XCD rather than once per
+// chunk, and every XCD streams one contiguous piece of the cache; with many
+// head groups (several queries over one cache) the groups of a chunk share an
+// L2 and its rows, and every XCD has work even when there are fewer chunks
+// than XCDs. Ids past the last item return at once (chunk >= num_chunks).
+__host__ __device__ inline int64_t mfma_grid_blocks(int num_chunks, int groups) {
+  return 8 * (((int64_t)num_chunks * groups + 7) / 8);
+}
 __device__ inline void block_coords(int num_chunks, int groups, int* chunk, int* group) {
   const int id = blockIdx.x;
-  const int per = (num_chunks + 7) / 8;
-  const int x = id & 7, k = id >> 3;
-  *group = k % groups;
-  *chunk = x * per + k / groups;
+  const int64_t per = ((int64_t)num_chunks * groups + 7) / 8;
+  const int64_t item = (id & 7) * per + (id >> 3);
+  *group = (int)(item % groups);
+  *chunk = (int)(item / groups);
 }
 
 // kFp8: FP8 E4M3 cache rows (KT = bf16: the tiles are expanded to bf16 in
@@ -1421,6 +1427,81 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
   }
 }
 
+// Copies-only variant of the attention kernel, for measuring the streaming
+// ceiling of its copy schedule: the same grid and block mapping
+// (block_coords), the same segment walk, and per tile the same 11 HBM->LDS
+// copies per wave (issue_tile_dma: c_t rows, k_rope, cos, sin; non-temporal
+// cache rows) into a ring of kRing tile buffers, with one barrier per tile and
+// no compute, LDS reads or stores. Iteration t issues tile t + kRing - 1 and
+// then waits for tile t + 1, so kRing - 1 tiles are in flight at the wait:
+// kRing = 3 is the attention kernel's ring (it keeps one tile in flight at
+// its end-of-iteration wait, two while it computes), kRing = 4 the deepest
+// ring 160 KB of LDS holds. 16-bit contiguous caches only.
+template <int kRing>
+__global__ __launch_bounds__(kThreads) void stream_copies_kernel(DecodeProblem p, int groups) {
+  static_assert(kRing >= 2 && kRing * kBufBytes + 2 * kT * 128 <= 160 * 1024, "ring fits the LDS");
+  constexpr uint32_t kCs = kRing * kBufBytes;  // one cos / sin buffer (never read)
+  extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
+  lchar* L = (lchar*)lds_raw;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  int chunk, group;
+  block_coords(p.num_chunks, groups, &chunk, &group);
+  if (chunk >= p.num_chunks) return;
+  const int64_t end_all = seq_begin(p, p.num_seqs);
+  int64_t lo = (int64_t)chunk * p.chunk_len;
+  const int64_t hi = min(lo + (int64_t)p.chunk_len, end_all);
+  lo = max(lo, seq_begin(p, 0));
+  if (lo >= hi) return;
+  int s = find_seq(p, lo);
+  while (lo < hi) {
+    const int64_t s_lo = seq_begin(p, s);
+    lo = max(lo, s_lo);
+    if (lo >= hi) break;
+    const int64_t s_hi = seq_end(p, s);
+    if (s_hi <= lo) {
+      if (++s >= p.num_seqs) break;
+      continue;
+    }
+    const int64_t seg_hi = min(hi, s_hi);
+    SegCtx sg;
+    sg.base = reinterpret_cast<const char*>(p.kv) + lo * kRowBytes;
+    sg.pos0 = lo - s_lo;
+    sg.last = (int)(seg_hi - lo - 1);
+    sg.seq = s;
+    sg.tab = nullptr;
+    sg.tile0 = 0;
+    const int ntiles = (sg.last + kT) / kT;
+    lds_barrier();
+    auto issue = [&](int k) {
+      const TileDma d = tile_dma<false>(sg, k, tile_base<false, false>(p, sg, k, 0), wave, lane_id());
+      const uint32_t buf = (uint32_t)(k % kRing) * kBufBytes;
+      const int lane = lane_id();
+      static_for<kDmaPerWave>([&](auto j) {
+        constexpr int J = decltype(j)::value;
+        if constexpr (J < 9) {
+          issue_copy<J>(p, sg, k, L, buf, wave, lane, d);
+        } else {  // cos / sin rows into the one table buffer
+          const int row = 8 * wave + (lane >> 3);
+          const int r = min(k * kT + row, sg.last);
+          const uint32_t toff = (uint32_t)(rope_row(p, sg.pos0 + r) * (kDr / 2) * 4 + (lane & 7) * 16);
+          const float* tab = J == 9 ? p.rope_cos : p.rope_sin;
+          __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(tab) + toff,
+                                           (lds_void*)(L + kCs + (J == 9 ? 0 : kT * 128) + 8 * wave * 128), 16, 0, 0);
+        }
+      });
+    };
+    for (int k = 0; k < kRing - 1; ++k) issue(k);
+    for (int t = 0; t < ntiles; ++t) {
+      lds_barrier();  // every wave is done with buffer (t - 1) % kRing
+      issue(t + kRing - 1);  // tiles past the segment re-read its last rows
+      wait_vm_ext<kDmaPerWave * (kRing - 2)>();  // this wave's copies of tile t + 1 have landed
+    }
+    wait_vm<0>();
+    lo = seg_hi;
+    ++s;
+  }
+}
+
 // q_prep = E([q_abs[row] (dc) | q_rope[row] (dR)] * scale_log2) in the
 // operand-order layout (qprep_index); row = s * Hq + hq. One thread per 8
 // consecutive elements (72 per row for dc = 512, dR = 64), i.e. per 16-B slot.
@@ -1467,7 +1548,7 @@ hipError_t launch_t(const DecodeProblem& p, hipStream_t stream, hipEvent_t ev_be
     attr_set = true;
   }
   const int groups = (p.Hq + kHG - 1) / kHG;
-  const int64_t blocks = (int64_t)((p.num_chunks + 7) / 8) * 8 * groups;
+  const int64_t blocks = mfma_grid_blocks(p.num_chunks, groups);
   if (ev_begin || ev_end) {
     // the events time this kernel's execution alone (no dispatch gap)
     hipExtLaunchKernelGGL((decode_mfma_kernel<KT, kPaged, kFp8>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes,
@@ -1525,6 +1606,23 @@ hipError_t launch_prep_q(const DecodeProblem& p, hipStream_t stream, float* zero
   else
     hipLaunchKernelGGL(prep_q_kernel<__half>, dim3(blocks), dim3(256), 0, stream, p.q_abs, p.q_rope, p.scale_log2,
                        reinterpret_cast<Ops<__half>::elem*>(p.q_prep), rows, p.Hq, zero_out, zero_n);
+  return hipGetLastError();
+}
+
+hipError_t launch_stream_copies(const DecodeProblem& p, int ring, hipStream_t stream) {
+  if (p.block_table || (p.kv_dtype != LA_DTYPE_BF16 && p.kv_dtype != LA_DTYPE_F16) || (ring != 3 && ring != 4))
+    return hipErrorInvalidValue;
+  const void* fn = ring == 3 ? reinterpret_cast<const void*>(&stream_copies_kernel<3>)
+                             : reinterpret_cast<const void*>(&stream_copies_kernel<4>);
+  const int lds = ring * kBufBytes + 2 * kT * 128;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (e != hipSuccess) return e;
+  const int groups = (p.Hq + kHG - 1) / kHG;
+  const int64_t blocks = mfma_grid_blocks(p.num_chunks, groups);
+  if (ring == 3)
+    hipLaunchKernelGGL(stream_copies_kernel<3>, dim3((unsigned)blocks), dim3(kThreads), lds, stream, p, groups);
+  else
+    hipLaunchKernelGGL(stream_copies_kernel<4>, dim3((unsigned)blocks), dim3(kThreads), lds, stream, p, groups);
   return hipGetLastError();
 }
 

@@ -85,6 +85,23 @@ class AppendArgs(ctypes.Structure):
     ]
 
 
+class PlanInfo(ctypes.Structure):
+    _fields_ = [
+        ("attention", ctypes.c_int32),
+        ("chunk_rows", ctypes.c_int32),
+        ("num_chunks", ctypes.c_int32),
+        ("num_slots", ctypes.c_int32),
+        ("head_groups", ctypes.c_int32),
+        ("merge", ctypes.c_int32),
+        ("absorb", ctypes.c_int32),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+LA_PLAN_ATTENTION_VALU, LA_PLAN_ATTENTION_MFMA = 1, 2
+LA_PLAN_MERGE_VALU, LA_PLAN_MERGE_MFMA, LA_PLAN_MERGE_MFMA_HALVES = 1, 2, 3
+LA_PLAN_ABSORB_NONE, LA_PLAN_ABSORB_VALU, LA_PLAN_ABSORB_MFMA, LA_PLAN_ABSORB_MFMA_QPREP = 0, 1, 2, 3
+
 _lib = None
 
 
@@ -114,6 +131,10 @@ def load() -> ctypes.CDLL:
     lib.la_mla_decode_profiled.argtypes = [ctypes.POINTER(DecodeArgs), vp, vp, vp, ctypes.c_int32]
     lib.la_mla_decode_noalloc_max_bytes.restype = sz
     lib.la_mla_decode_noalloc_max_bytes.argtypes = []
+    lib.la_mla_decode_plan.restype = i32
+    lib.la_mla_decode_plan.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.POINTER(PlanInfo)]
+    lib.la_stream_ceiling.restype = i32
+    lib.la_stream_ceiling.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.c_int32, vp, vp, vp, ctypes.c_int32]
     lib.la_fused_mla.restype = i32
     lib.la_fused_mla.argtypes = [vp, i32, i32, vp, vp, vp, i32, vp, vp, vp, cfgp, vp, sz, vp]
     lib.la_batched_fused_mla.restype = i32

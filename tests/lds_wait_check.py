@@ -63,14 +63,49 @@ def _retire(pend: list, k: int) -> list:
     return [] if k == 0 else (pend[len(pend) - k:] if k < len(pend) else pend)
 
 
+def _dead_high_half_read(instrs: list, n: int, pending: set) -> bool:
+    """True when instruction n is a v_mad_u64_u32 whose only pending register
+    is the high half of its 64-bit addend and whose result's high half is
+    overwritten (next in program text) before anything reads it: the low 32 bits of a*b + c depend
+    only on the low 32 bits of c, so the stale high half cannot reach a use.
+    (The compiler forms such 64-bit addends from a 32-bit value and whatever
+    the next register holds when it only keeps the low half of the sum.)"""
+    ins = instrs[n]
+    if ins.split()[0] != "v_mad_u64_u32":
+        return False
+    ops = _operands(ins)
+    if len(ops) < 5:
+        return False
+    dst, addend = _regs(ops[0]), sorted(_regs(ops[4]))
+    if len(addend) != 2 or (_regs(ops[4]) & pending) != {addend[1]}:
+        return False
+    if (_regs(ops[2]) | _regs(ops[3])) & pending:
+        return False
+    hi = max(dst)
+    # like the rest of this module, the walk is linear: the next instruction
+    # in program text that names the high half must overwrite it
+    for later in instrs[n + 1:]:
+        op = later.split()[0]
+        if op.startswith(("s_setpc", "s_endpgm")):
+            return False
+        lops = _operands(later)
+        reads = set()
+        for o in (lops[1:] if lops else []):
+            reads |= _regs(o)
+        if hi in reads:
+            return False
+        if lops and hi in _regs(lops[0]) and not op.startswith(("ds_", "global_", "buffer_")):
+            return True  # overwritten by a VALU result before any read
+    return False
+
+
 def pending_uses(instrs: list, counters=("lgkm",)) -> list:
     """Instructions that touch a register an unretired LDS read (counter
     "lgkm") or vector-memory load ("vm") will write. Vector-memory operations
     are modelled like LDS operations with their own in-order counter (stores
-    and HBM->LDS copies count without a destination). The vm model also
-    reports reads the compiler makes of an unused register half (the high half
-    of a v_mad_u64_u32 addend whose result it truncates), which are harmless,
-    so the kernel test applies only the lgkm model."""
+    and HBM->LDS copies count without a destination). A v_mad_u64_u32 that
+    reads only the unused high half of a pending 64-bit addend
+    (_dead_high_half_read) is not reported."""
     pend = {"lgkm": [], "vm": []}  # counter -> [(destination registers, index)]
     bad = []
     for n, ins in enumerate(instrs):
@@ -90,7 +125,7 @@ def pending_uses(instrs: list, counters=("lgkm",)) -> list:
             used |= _regs(o)
         for cnt in counters:
             for dest, at in pend[cnt]:
-                if dest & used:
+                if dest & used and not _dead_high_half_read(instrs, n, dest & used):
                     bad.append((n, ins, at, instrs[at]))
         if op.startswith("ds_"):
             pend["lgkm"].append((_regs(ops[0]) if op.startswith("ds_read") else set(), n))

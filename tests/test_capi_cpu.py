@@ -38,7 +38,8 @@ def test_ctypes_structs_match_the_header(tmp_path):
     if gcc is None:
         pytest.skip("gcc not available")
     REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    structs = {"la_decode_args": capi.DecodeArgs, "la_append_args": capi.AppendArgs}
+    structs = {"la_decode_args": capi.DecodeArgs, "la_append_args": capi.AppendArgs,
+               "la_plan_info": capi.PlanInfo}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "latent_attn.h"', "int main(void) {"]
     for cname, py in structs.items():
         lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -161,6 +162,49 @@ def test_profiled_decode_rejects_a_negative_repeat():
     assert lib.la_mla_decode_profiled(ctypes.byref(a), None, None, None, 10) == capi.LA_ERROR_INVALID_VALUE
 
 
+def test_plan_query_without_a_gfx950_device():
+    """la_mla_decode_plan reports the plan la_mla_decode would run. Without a
+    gfx950 device (this host) the MFMA attention kernel is not selectable:
+    the VALU kernel's plan aims at 4 workgroups per CU (256 CUs assumed) over
+    one workgroup per query head. Config 3's shape (32 sequences x 8,192 rows,
+    128 heads): 1,024 / 128 = 8 chunks of 32,768 rows, 8 + 32 - 1 = 39 slots
+    per head; fp32 partials, merged and projected on the MFMA merge; q_nope
+    absorbed on the MFMA absorb kernel into fp32 queries."""
+    lib = capi.load()
+    a = _args(num_seqs=32, seq_len=8192, total_rows=32 * 8192, q_absorbed=0, q_nope=0x2000, W_UK=0x3000)
+    info = capi.PlanInfo()
+    assert lib.la_mla_decode_plan(ctypes.byref(a), ctypes.byref(info)) == capi.LA_SUCCESS
+    assert (info.attention, info.chunk_rows, info.num_chunks, info.num_slots, info.head_groups) == (
+        capi.LA_PLAN_ATTENTION_VALU, 32768, 8, 39, 128)
+    assert (info.merge, info.absorb) == (capi.LA_PLAN_MERGE_MFMA, capi.LA_PLAN_ABSORB_MFMA)
+    al = lambda x: (x + 255) // 256 * 256
+    want = al(32 * 128 * 512 * 4) + al(39 * 128 * 512 * 4) + al(39 * 128 * 4)  # q_abs, fp32 partials, lse
+    assert info.workspace_bytes == want == lib.la_mla_decode_workspace_size(ctypes.byref(a))
+    # pre-absorbed queries: no absorb step; an empty batch: an empty plan
+    b = _args(num_seqs=32, seq_len=8192, total_rows=32 * 8192)
+    assert lib.la_mla_decode_plan(ctypes.byref(b), ctypes.byref(info)) == capi.LA_SUCCESS
+    assert info.absorb == capi.LA_PLAN_ABSORB_NONE
+    e = _args(num_seqs=0)
+    assert lib.la_mla_decode_plan(ctypes.byref(e), ctypes.byref(info)) == capi.LA_SUCCESS
+    assert (info.attention, info.num_chunks, info.workspace_bytes) == (0, 0, 0)
+    assert lib.la_mla_decode_plan(ctypes.byref(_args(queries_per_seq=0)), ctypes.byref(info)) == \
+        capi.LA_ERROR_INVALID_VALUE
+    assert lib.la_mla_decode_plan(ctypes.byref(a), None) == capi.LA_ERROR_INVALID_VALUE
+
+
+def test_stream_ceiling_rejects_bad_arguments():
+    """la_stream_ceiling (the copies-only measurement of the attention
+    kernel's copy schedule) checks its ring depth, repeat count and
+    descriptor before any device work."""
+    lib = capi.load()
+    a = _args()
+    for ring in (0, 2, 5):
+        assert lib.la_stream_ceiling(ctypes.byref(a), ring, None, None, None, 1) == capi.LA_ERROR_INVALID_VALUE
+    assert lib.la_stream_ceiling(ctypes.byref(a), 3, None, None, None, -1) == capi.LA_ERROR_INVALID_VALUE
+    a = _args(queries_per_seq=0)
+    assert lib.la_stream_ceiling(ctypes.byref(a), 3, None, None, None, 1) == capi.LA_ERROR_INVALID_VALUE
+
+
 def test_decode_rejects_bad_config():
     lib = capi.load()
     a = _args()
@@ -206,7 +250,7 @@ def test_extension_requires_device_tensors():
 
 def test_extension_dtype_and_layout_messages():
     cfg, kv, qa, qr, W, c = _fused_inputs()
-    with pytest.raises(RuntimeError, match="kv_cache must be float16, bfloat16 or float32"):
+    with pytest.raises(RuntimeError, match="kv_cache must be float16, bfloat16, float32 or float8_e4m3fn"):
         F.fused_mla(kv.to(torch.int32), qa, qr, W, c, c, cfg)
     with pytest.raises(RuntimeError, match="kv_cache must be contiguous"):
         F.fused_mla(kv.t(), qa, qr, W, c, c, cfg)

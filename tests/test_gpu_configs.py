@@ -116,6 +116,10 @@ def test_config2_merge_halves_repeat_bitwise(cuda, abi):
     onto zero give fl(a + b) in either order: repeated calls are bitwise equal."""
     lib, capi = abi
     inp = bench.build_inputs("cfg2", cuda)
+    out = torch.empty(1, inp["cfg"].num_heads, inp["cfg"].v_head_dim, device=cuda)
+    info = capi.PlanInfo()
+    assert lib.la_mla_decode_plan(ctypes.byref(bench.decode_args(inp, out, capi)), ctypes.byref(info)) == 0
+    assert info.merge == capi.LA_PLAN_MERGE_MFMA_HALVES, info.merge  # the path this test is about
     outs = [_run(inp, lib, capi) for _ in range(4)]
     print("[cfg2] four calls, merge over latent halves", flush=True)
     for o in outs[1:]:
@@ -149,47 +153,105 @@ def test_config2_plan_keeps_partials_below_cache(cuda, abi):
     assert lib.la_mla_decode_workspace_size(ctypes.byref(a)) > cache_bytes
 
 
-def _plan_workspace(B, total, Hq, ncu, chunk_rows=0):
-    """Workspace of the MFMA split plan (q_nope absorbed into 16-bit queries):
-    about one workgroup per CU, chunks of at least ceil(Hq*512/576) rows
-    rounded up to 64; slots = chunks + sequences - 1; regions 256-B aligned:
-    [q_prep (B, Hq padded to 32, 576) 16-bit] [partials (slots*Hq, 512) fp16]
-    [scales (2) and maxima (1) fp32 per partial row] [log-sum-exps fp32]."""
-    def al(x):
-        return (x + 255) // 256 * 256
+def _al(x):
+    return (x + 255) // 256 * 256
 
-    if chunk_rows:
-        L = chunk_rows
-    else:
-        chunks = max(1, ncu // ((Hq + 127) // 128))
-        L = -(-total // chunks)
-        L = max(L, -(-(Hq * 512) // 576))
-        L = max(-(-L // 64) * 64, 64)
-    n = -(-total // L)
-    slots = n + B - 1
-    q_prep = al(B * (-(-Hq // 32) * 32) * 576 * 2)
-    return q_prep + al(slots * Hq * 512 * 2) + al(slots * Hq * 3 * 4) + al(slots * Hq * 4), L, n
+
+def _mfma_workspace(B, Hq, slots):
+    """Workspace of an MFMA plan whose queries become the attention kernel's
+    16-bit rows: [q_prep (B, Hq padded to 32, 576) 16-bit] [partials
+    (slots * Hq, 512) fp16] [2 scales + 1 maximum fp32 per partial row]
+    [log-sum-exp fp32 per partial row], each region 256-B aligned."""
+    return (_al(B * (-(-Hq // 32) * 32) * 576 * 2) + _al(slots * Hq * 512 * 2) + _al(slots * Hq * 3 * 4) +
+            _al(slots * Hq * 4))
+
+
+# Hand-computed plans on a 256-CU MI355X (one 128-head group per chunk unless
+# noted): about one workgroup per CU, chunks rounded up to 64 rows and at
+# least 128 rows for a 128-head group (its 128 fp16 partial rows, 128 KB,
+# stay below the 16-bit cache bytes it streams, 114 rows); slots = chunks +
+# sequences - 1; the latent-half merge when the full-row merge would have
+# fewer than 256 workgroups (8 x ceil(128 / 8) x ceil(query rows / 16)).
+#   name: (chunk_rows, num_chunks, num_slots, head_groups, merge)
+_HALVES, _FULL = 3, 2
+PLANS_256 = {
+    # 8,192 rows / 256 = 32 -> 128-row floor: 64 chunks; 1 query row: 128 merge workgroups
+    "cfg2": (128, 64, 64, 1, _HALVES),
+    # 262,144 / 256 = 1,024; 32 rows -> 256 merge workgroups
+    "cfg3": (1024, 256, 287, 1, _FULL),
+    # 1,033,074 ragged rows / 256 = 4,035.4 -> 4,096: 253 chunks, + 63 slots; 64 rows -> 512
+    "cfg4": (4096, 253, 316, 1, _FULL),
+    # 524,288 / 256 = 2,048; 4 rows -> 128 merge workgroups
+    "cfg5": (2048, 256, 259, 1, _HALVES),
+}
 
 
 @pytest.mark.parametrize("name", ["cfg2", "cfg3", "cfg4", "cfg5"])
 def test_mfma_plan_at_the_benchmark_configs(cuda, abi, name):
-    """The split plan on the benchmark configurations, pinned by its workspace:
-    one workgroup per CU where the rows allow (config 3: 256 chunks of 1,024
-    rows, config 5: 256 of 2,048, config 4: 253 chunks over the ragged rows),
-    and at B = 1 the 128-row floor that keeps the partial rows below the
-    cache bytes (64 chunks)."""
+    """The split plan on the benchmark configurations against hand-computed
+    values (la_mla_decode_plan), and its workspace."""
     lib, capi = abi
+    ncu = torch.cuda.get_device_properties(cuda).multi_processor_count
+    if ncu != 256:
+        pytest.skip(f"hand-computed plans assume 256 CUs, device has {ncu}")
     inp = bench.build_inputs(name, cuda)
     cfg = inp["cfg"]
     out = torch.empty(inp["B"], cfg.num_heads, cfg.v_head_dim, device=cuda)
     a = bench.decode_args(inp, out, capi)
+    info = capi.PlanInfo()
+    assert lib.la_mla_decode_plan(ctypes.byref(a), ctypes.byref(info)) == 0
+    got = (info.chunk_rows, info.num_chunks, info.num_slots, info.head_groups, info.merge)
+    print(f"[plan {name}] {got}, workspace {info.workspace_bytes} B", flush=True)
+    assert info.attention == capi.LA_PLAN_ATTENTION_MFMA and info.absorb == capi.LA_PLAN_ABSORB_MFMA_QPREP
+    assert got == PLANS_256[name]
+    assert info.workspace_bytes == _mfma_workspace(inp["B"], cfg.num_heads, info.num_slots)
+    assert info.workspace_bytes == lib.la_mla_decode_workspace_size(ctypes.byref(a))
+    if name == "cfg2":
+        # an FP8 cache: the floor counts rows, so the same chunks (its partials
+        # may reach twice the fp8 cache bytes); and the explicit 64-row
+        # override still works, with the larger workspace
+        a.kv_dtype = capi.LA_DTYPE_FP8_E4M3
+        assert lib.la_mla_decode_plan(ctypes.byref(a), ctypes.byref(info)) == 0
+        assert (info.chunk_rows, info.num_chunks) == (128, 64)
+        a.kv_dtype = capi.LA_DTYPE_BF16
+        a.chunk_rows = 64
+        assert lib.la_mla_decode_plan(ctypes.byref(a), ctypes.byref(info)) == 0
+        assert (info.chunk_rows, info.num_chunks) == (64, 128)
+        assert info.workspace_bytes > 8192 * 1152  # partials above the cache bytes
+
+
+@pytest.mark.parametrize("batch,seq_len,want", [
+    # the reference's batched entry (B queries over one shared cache, Hq = 128 B):
+    # B = 16 at 2,048 rows: 16 head groups -> 256 / 16 = 16 chunks of 128 rows
+    # (the 128-row floor of one group), 16 query rows -> 128 merge workgroups
+    (16, 2048, (128, 16, 16, 16, _HALVES)),
+    # B = 64 at 8,192 rows: 64 groups -> 4 chunks of 2,048 rows, 64 rows -> 512
+    (64, 8192, (2048, 4, 4, 64, _FULL)),
+    # B = 1 at 512 rows: 4 chunks of the 128-row floor
+    (1, 512, (128, 4, 4, 1, _HALVES)),
+])
+def test_mfma_plan_for_the_shared_cache_entry(cuda, abi, batch, seq_len, want):
+    """la_batched_fused_mla's plan: the row floor applies per 128-head group
+    (each group's workgroup writes its own 128 partial rows), not to all
+    128 B heads at once, which made 1,856-row chunks and 32 workgroups at
+    B = 16."""
+    lib, capi = abi
     ncu = torch.cuda.get_device_properties(cuda).multi_processor_count
-    want, L, n = _plan_workspace(inp["B"], int(inp["total"]), cfg.num_heads, ncu)
-    got = lib.la_mla_decode_workspace_size(ctypes.byref(a))
-    print(f"[plan {name}] {ncu} CUs: {n} chunks of {L} rows, workspace {got} B", flush=True)
+    if ncu != 256:
+        pytest.skip(f"hand-computed plans assume 256 CUs, device has {ncu}")
+    a = capi.DecodeArgs()
+    fake = 0x10000
+    a.kv_cache, a.kv_dtype, a.total_rows, a.num_seqs, a.seq_len = fake, capi.LA_DTYPE_F16, seq_len, 1, seq_len
+    a.queries_per_seq, a.q_absorbed, a.q_rope = batch, fake, fake
+    a.W_UV, a.w_uv_dtype, a.rope_cos, a.rope_sin, a.rope_rows, a.output = fake, capi.LA_DTYPE_F16, fake, fake, 0, fake
+    from latent_attn import MLAConfig
+    a.cfg = capi.config(MLAConfig.deepseek_v2())
+    info = capi.PlanInfo()
+    assert lib.la_mla_decode_plan(ctypes.byref(a), ctypes.byref(info)) == 0
+    got = (info.chunk_rows, info.num_chunks, info.num_slots, info.head_groups, info.merge)
+    print(f"[plan shared B={batch} S={seq_len}] {got}", flush=True)
+    assert info.attention == capi.LA_PLAN_ATTENTION_MFMA and info.absorb == capi.LA_PLAN_ABSORB_NONE
     assert got == want
-    if name in ("cfg3", "cfg5"):
-        assert n == ncu
 
 
 def test_config3_batched_uniform(cuda, abi):

@@ -273,6 +273,13 @@ def test_extension_checks_on_device(cuda):
                              128)
     with pytest.raises(RuntimeError, match="rope_cos / rope_sin need at least"):
         F.fused_mla(kv, torch.zeros(128, 512, device=cuda), q_rope, W_UV, cos[:10], sin[:10], cfg)
+    # FP8 E4M3 is a cache format only: an fp8 weight is refused with the
+    # weights' message, an int cache with the caches' message (which names fp8)
+    qa = torch.zeros(128, 512, device=cuda)
+    with pytest.raises(RuntimeError, match="W_UV must be float16, bfloat16 or float32, got"):
+        F.fused_mla(kv, qa, q_rope, W_UV.to(torch.float8_e4m3fn), cos, sin, cfg)
+    with pytest.raises(RuntimeError, match="kv_cache must be float16, bfloat16, float32 or float8_e4m3fn"):
+        F.fused_mla(kv.to(torch.int16), qa, q_rope, W_UV, cos, sin, cfg)
 
 
 # ---------------------------------------------------------------------------

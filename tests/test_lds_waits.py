@@ -1,9 +1,13 @@
 """CPU check of the compiled attention kernels: no instruction touches a
-register that an inline-asm LDS read has not yet written (see
-tests/lds_wait_check.py). Compiles latent-attn_amd/csrc/la_mfma.hip for
+register that an inline-asm LDS read (lgkmcnt) or vector-memory load
+(vmcnt: the 36 query loads of the prologue, waited for by hand-counted
+vmcnt values, and the paged cache's block-table entries) has not yet written
+(see tests/lds_wait_check.py). Compiles latent-attn_amd/csrc/la_mfma.hip for
 gfx950 to assembly with hipcc (about half a minute) and checks every
 instantiation of decode_mfma_kernel. A compiler copy of such a register
-before its wait once read a partner wave's rescale flag before it had landed.
+before its wait once read a partner wave's rescale flag before it had landed;
+a count that released a wait early would show up the same way, as a use of a
+register whose load the in-order model has not retired.
 """
 
 from __future__ import annotations
@@ -43,8 +47,25 @@ def test_checker_catches_an_early_copy():
     assert [b[0] for b in pending_uses(counted)] == [4]
 
 
-def test_no_register_touched_before_its_lds_wait(decode_kernels):
+def test_checker_models_vector_memory_loads():
+    # a copy of a pending query-load register, before and after a counted wait
+    loads = ["global_load_dwordx4 v[0:3], v[10:11], off", "global_load_dwordx4 v[4:7], v[10:11], off",
+             "v_mov_b32_e32 v20, v1", "s_waitcnt vmcnt(1)", "v_mov_b32_e32 v21, v2", "v_mov_b32_e32 v22, v5"]
+    assert [b[0] for b in pending_uses(loads, counters=("vm",))] == [2, 5]
+    # HBM->LDS copies count without a destination: vmcnt(1) retires the load, not the copy
+    mixed = ["global_load_dword v205, v[0:1], off", "global_load_lds_dwordx4 v[2:3], off",
+             "s_waitcnt vmcnt(1)", "v_mov_b32_e32 v7, v205"]
+    assert pending_uses(mixed, counters=("vm",)) == []
+    # a 64-bit addend whose pending high half only feeds the dropped high half of the result
+    dead = ["global_load_dword v205, v[0:1], off", "v_mad_u64_u32 v[192:193], vcc, v192, s96, v[204:205]",
+            "v_mov_b32_e32 v193, 0"]
+    assert pending_uses(dead, counters=("vm",)) == []
+    used = dead[:2] + ["v_mov_b32_e32 v7, v193"]
+    assert [b[0] for b in pending_uses(used, counters=("vm",))] == [1]
+
+
+def test_no_register_touched_before_its_wait(decode_kernels):
     for name, instrs in decode_kernels.items():
-        bad = pending_uses(instrs)
+        bad = pending_uses(instrs, counters=("lgkm", "vm"))
         assert not bad, f"{name}: " + "; ".join(f"#{n} {ins!r} before the wait of #{at} {rd!r}"
                                                for n, ins, at, rd in bad[:5])

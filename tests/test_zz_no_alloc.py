@@ -103,3 +103,46 @@ def test_noalloc_refuses_a_step_beyond_its_scratch(cuda):
     a.cfg = capi.config(cfg)
     assert lib.la_mla_decode_workspace_size(ctypes.byref(a)) > lib.la_mla_decode_noalloc_max_bytes()
     assert lib.la_mla_decode_noalloc(ctypes.byref(a), None) == capi.LA_ERROR_WORKSPACE
+
+
+def test_noalloc_under_hip_graph_capture(cuda):
+    """la_mla_decode_noalloc captured into a HIP graph (torch.cuda.graph on a
+    side stream) after one eager warm-up call (which looks up the scratch
+    address and sets the kernels' attributes: the only non-stream HIP calls on
+    the path). Every replay, with eager work and a synchronisation between
+    replays (a la_mla_decode call with a caller workspace, and the output
+    refilled with NaN), equals the eager la_mla_decode output bit for bit.
+    Nothing on this path records a memset (the latent-half merge's output is
+    zeroed by the absorb kernel)."""
+    lib = capi.load()
+    cfg = MLAConfig.deepseek_v2()
+    stream = torch.cuda.current_stream().cuda_stream
+    W_UK, W_UV = make_weights(cfg, "bf16", 211, cuda)
+    B, S = 8, 2048
+    kv = make_cache((B * S,), cfg, "bf16", 212, cuda)
+    q_nope, q_rope = make_queries((B,), cfg, 213, cuda)
+    cos, sin = rope(S, cfg, cuda)
+    out = torch.empty(B, 128, 128, device=cuda)
+    a = _args(kv, None, S, q_nope, q_rope, W_UK, W_UV, cos, sin, out, cfg)
+    want, got = _both(lib, a, out, stream)  # eager reference and the warm-up noalloc call
+    assert torch.equal(got, want)
+    side = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    print("[noalloc] capturing into a HIP graph", flush=True)
+    with torch.cuda.graph(g, stream=side):
+        st = lib.la_mla_decode_noalloc(ctypes.byref(a), ctypes.c_void_p(side.cuda_stream))
+    assert st == capi.LA_SUCCESS, lib.la_status_string(st)
+    need = lib.la_mla_decode_workspace_size(ctypes.byref(a))
+    ws = torch.empty(need, dtype=torch.uint8, device=cuda)
+    other = torch.empty_like(out)
+    b = _args(kv, None, S, q_nope, q_rope, W_UK, W_UV, cos, sin, other, cfg)
+    b.workspace, b.workspace_bytes = ws.data_ptr(), need
+    for r in range(4):
+        out.fill_(float("nan"))
+        assert lib.la_mla_decode(ctypes.byref(b), ctypes.c_void_p(stream)) == capi.LA_SUCCESS  # eager work
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"[noalloc] replay {r}", flush=True)
+        assert torch.equal(out, want), (r, float((out - want).abs().max()))
+        assert torch.equal(other, want)
