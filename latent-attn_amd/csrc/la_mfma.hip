@@ -379,6 +379,11 @@ __device__ inline void lds_st(lchar* L, uint32_t off, T v) {
 __device__ inline void st_global_dev16(void* p, i16x8 v) {
   asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
+// The same policy on buffer stores (the cache-policy operand's sc1 bit), and
+// word 3 of a raw buffer resource (32-bit data format, as the gfx9 family
+// expects).
+constexpr int kCpolSc1 = 16;
+constexpr int kBufferRsrcWord3 = 0x00020000;
 // ds_read_b64_tr_b16 as inline asm: the builtin makes the compiler assume the
 // read may alias the in-flight HBM->LDS copies and drain vmcnt before it. OFF
 // is the instruction's immediate byte offset. The result must not be used
@@ -871,6 +876,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
   typedef typename O_::vec vec;
   typedef typename O_::elem E;
 
+  warm_kernarg_lines(p);
   extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
   lchar* L = (lchar*)lds_raw;
   const int tid = threadIdx.x, lane0 = tid & 63;
@@ -1415,12 +1421,32 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       asm volatile("" : "+v"(xr[8]), "+v"(xr[9]), "+v"(xr[10]), "+v"(xr[11]), "+v"(xr[12]), "+v"(xr[13]), "+v"(xr[14]), "+v"(xr[15]));
       asm volatile("" : "+v"(xr[16]), "+v"(xr[17]), "+v"(xr[18]), "+v"(xr[19]), "+v"(xr[20]), "+v"(xr[21]), "+v"(xr[22]), "+v"(xr[23]));
       asm volatile("" : "+v"(xr[24]), "+v"(xr[25]), "+v"(xr[26]), "+v"(xr[27]), "+v"(xr[28]), "+v"(xr[29]), "+v"(xr[30]), "+v"(xr[31]));
-      static_for<32>([&](auto j_c) {
-        constexpr int j = decltype(j_c)::value;
-        const int r = 2 * j + (lr >> 5);                       // staged row
-        const int hb = r < 32 ? 32 * wave + r : 32 * pw + (r - 32);  // head within the group
-        if (hb < hg_heads) st_global_dev16(obase + (uint32_t)(hb * kDc), xr[j]);
-      });
+      if (hg_heads == kHG) {
+        // a full group (every benchmark shape): no row to mask, so each
+        // store is the lane offset plus a wave-uniform row offset in an
+        // SGPR, with no per-store exec mask or address arithmetic
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<_Float16*>(p.part_o) + hqg * kDc, 0, kHG * kDc * 2, kBufferRsrcWord3);
+        const int vlane = (lr >> 5) * (kDc * 2) + 512 * ch + 16 * (lr & 31);
+        // row offsets of staged rows 0 and 32 (own heads, then the
+        // partner's), made here (the empty asm) so the per-store offsets
+        // below are one scalar add each rather than 32 values computed at
+        // kernel start and held in spill slots
+        int own = 32 * wave * (kDc * 2), par = 32 * pw * (kDc * 2);
+        asm volatile("" : "+s"(own), "+s"(par));
+        static_for<32>([&](auto j_c) {
+          constexpr int j = decltype(j_c)::value;
+          const int soff = j < 16 ? own + 2 * j * (kDc * 2) : par + 2 * (j - 16) * (kDc * 2);  // staged rows 2j, 2j+1
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xr[j]), rsrc, vlane, soff, kCpolSc1);
+        });
+      } else {
+        static_for<32>([&](auto j_c) {
+          constexpr int j = decltype(j_c)::value;
+          const int r = 2 * j + (lr >> 5);                             // staged row
+          const int hb = r < 32 ? 32 * wave + r : 32 * pw + (r - 32);  // head within the group
+          if (hb < hg_heads) st_global_dev16(obase + (uint32_t)(hb * kDc), xr[j]);
+        });
+      }
     }
     lo = seg_hi;
     ++s;

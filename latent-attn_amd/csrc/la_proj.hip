@@ -472,6 +472,7 @@ constexpr int kMPOPitch = kDcP + 8;
 
 template <typename WT, bool F16>
 __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProblem p) {
+  warm_kernarg_lines(p);
   typedef Mma16<WT> M;
   typedef typename M::vec vec;
   constexpr float kLoScale = Mma<WT>::kLoScale;
@@ -583,6 +584,7 @@ constexpr int kMPHSum = 256 + 4;    // floats per LDS row of a slot-group sum
 
 template <typename WT>
 __global__ __launch_bounds__(kMPWaves * 64) void merge_project_half_kernel(DecodeProblem p) {
+  warm_kernarg_lines(p);
   typedef Mma16<WT> M;
   typedef typename M::vec vec;
   typedef typename Mma<WT>::elem E;
