@@ -99,6 +99,9 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
                                                           float* __restrict__ zero_out, int64_t zero_n) {
   typedef Mma<WT> M;
   typedef typename M::vec vec;
+  // both 64-B scalar-cache lines of the arguments in one round of loads (see
+  // warm_kernarg_lines)
+  asm volatile("" ::"s"(tokens), "s"(qps));
   __shared__ __attribute__((aligned(16))) char wt[128 * kAbsRowBytes];  // dn <= 128 rows
   // q operands (hi, lo) of the 8 k-steps, shared by the 4 waves: [ks][hi|lo][lane] 16 B
   __shared__ __attribute__((aligned(16))) char qs[8 * 2 * 64 * 16];
@@ -129,11 +132,14 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
   const int t = t0 + (lane & 31);
   const bool tvalid = t < tokens;
   const float* qrow = q_nope + ((int64_t)(tvalid ? t : 0) * nh + h) * dn + 8 * (lane >> 5);
+  // (with NKS > 0 every wave's two k-steps exist: the loads go out
+  // unconditionally, since a load under a branch gets its result copied at
+  // the branch's end, which waits for it before the W_UK loads below issue)
   f32x4 qa[2], qb[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int ks = 2 * wave + j;
-    if (ks < nks) {
+    if (NKS > 0 || ks < nks) {
       qa[j] = *reinterpret_cast<const f32x4*>(qrow + 16 * ks);
       qb[j] = *reinterpret_cast<const f32x4*>(qrow + 16 * ks + 4);
     }
@@ -154,7 +160,7 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int ks = 2 * wave + j;
-    if (ks < nks) {
+    if (NKS > 0 || ks < nks) {
       float x[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
