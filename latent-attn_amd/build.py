@@ -9,8 +9,12 @@
 * ``tests/cpp/reference_caller`` -- the C++ drop-in test program (a caller
   of include/fused_mla.cuh written like the reference's C++ test), run by
   tests/test_gpu_cpp_caller.py.
+* with ``--phase-stamps`` only: ``_build/phase/liblatent_attn_hip.so``, the
+  same sources compiled with -DLA_PHASE_STAMPS (kernels that record clock
+  stamps at their phase boundaries), read by latent-attn_amd/phase_profile.py.
+  It is a measurement build, never loaded by the package.
 
-Usage: ``python latent-attn_amd/build.py [--lib-only]``. Always recompiles.
+Usage: ``python latent-attn_amd/build.py [--lib-only] [--phase-stamps]``. Always recompiles.
 """
 
 from __future__ import annotations
@@ -53,17 +57,22 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}")
 
 
-def build_lib(jobs: int = 8) -> str:
-    os.makedirs(BUILD, exist_ok=True)
+PHASE_LIB = os.path.join(BUILD, "phase", LIB_NAME)
+
+
+def build_lib(jobs: int = 8, phase_stamps: bool = False) -> str:
+    bdir = os.path.join(BUILD, "phase") if phase_stamps else BUILD
+    os.makedirs(bdir, exist_ok=True)
     objs = []
     cmds = []
+    extra = ["-DLA_PHASE_STAMPS"] if phase_stamps else []
     for src in HIP_SOURCES:
-        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        obj = os.path.join(bdir, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([HIPCC, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
     with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(cmds)))) as ex:
         list(ex.map(_run, cmds))
-    out = os.path.join(PKG, LIB_NAME)
+    out = PHASE_LIB if phase_stamps else os.path.join(PKG, LIB_NAME)
     tmp = out + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, out)
@@ -120,5 +129,8 @@ def build(lib_only: bool = False) -> None:
 
 
 if __name__ == "__main__":
-    build(lib_only="--lib-only" in sys.argv)
-    print("built", os.path.join(PKG, LIB_NAME))
+    if "--phase-stamps" in sys.argv:
+        print("built", build_lib(phase_stamps=True))
+    else:
+        build(lib_only="--lib-only" in sys.argv)
+        print("built", os.path.join(PKG, LIB_NAME))

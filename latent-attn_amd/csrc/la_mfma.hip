@@ -51,6 +51,32 @@
 #include <type_traits>
 
 namespace la {
+
+// Phase-timing build only (-DLA_PHASE_STAMPS: build.py --phase-stamps, read
+// by phase_profile.py; the shipped library has none of it). Every wave of
+// the attention kernel records the shader clock (s_memtime) at the phase
+// boundaries of its last segment and writes the 11 values at exit:
+//   0 entry (after the first round of argument loads)  1 segment set up
+//   2 past the segment's opening barrier  3 Q loads issued
+//   4 tile 0 landed  5 tile 0 rotated  6 loop at t = 0 (after iteration -1)
+//   7 loop done  8 past the staging barrier  9 partial stores issued
+//   10 stores complete
+// A stamp waits for the scalar data path (lgkmcnt), which drains the wave's
+// LDS queue: the instrumented kernel runs a few per cent slower.
+#ifdef LA_PHASE_STAMPS
+constexpr int kStampSlots = 12;
+constexpr int kStampBlocks = 4096;
+__device__ unsigned long long g_attn_stamps[kStampBlocks * 4 * kStampSlots];
+#define LA_STAMP(i)                                                                                  \
+  do {                                                                                               \
+    unsigned long long t_;                                                                           \
+    asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t_)::"memory");                       \
+    stamps_[i] = t_;                                                                                 \
+  } while (0)
+#else
+#define LA_STAMP(i) ((void)0)
+#endif
+
 namespace {
 
 constexpr int kDc = 512;
@@ -876,6 +902,10 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
   typedef typename O_::vec vec;
   typedef typename O_::elem E;
 
+#ifdef LA_PHASE_STAMPS
+  unsigned long long stamps_[kStampSlots] = {};
+#endif
+  LA_STAMP(0);
   warm_kernarg_lines(p);
   extern __shared__ __attribute__((aligned(1024))) char lds_raw[];
   lchar* L = (lchar*)lds_raw;
@@ -913,7 +943,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     const int seg_len = sg.last + 1;
     const int ntiles = (seg_len + kT - 1) / kT;
 
+    LA_STAMP(1);
     lds_barrier();  // all waves are done with the previous segment's buffers
+    LA_STAMP(2);
 
     // paged cache: the table entries of tiles 0 and 1 (tile 1 is copied in
     // iteration -1); iteration t loads the entry of tile t+3 into blk_cur once
@@ -957,6 +989,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
 #pragma unroll
       for (int kk = 0; kk < 36; ++kk) asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(qb[kk]) : "v"(qsrc + 64 * kk));
     }
+    LA_STAMP(3);
 
     float m_run = -INFINITY, l_run = 0.f;
     // O = 0, written by MFMAs of zero operands straight into the AGPRs (a
@@ -970,8 +1003,10 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     }
 
     wait_vm_ext<36>();  // tile 0's copies have landed (the 36 Q loads went out after them)
+    LA_STAMP(4);
     rotate_rows<KT, kFp8>(L, 0, wave, lane_id());  // fresh lane index: no spilled addresses
     if constexpr (kFp8) expand_rows(L, 0, wave, lane_id());
+    LA_STAMP(5);
 
     // Software pipeline over tiles; iteration t (from -1):
     //   [apply the rescale of own-head O rows decided by softmax(t)]
@@ -1010,6 +1045,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       }
     }
     for (int t = -1; t < ntiles; ++t) {
+#ifdef LA_PHASE_STAMPS
+      if (t == 0) LA_STAMP(6);
+#endif
       // this wave's copies of tile t+1 were waited for at the end of
       // iteration t-1 (t = -1: tile 0 in the prologue; the Q loads are still
       // in flight and QK(0) waits for them group by group)
@@ -1341,6 +1379,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       if constexpr (kPaged) tie(blk_cur);  // and the table entry loaded with them
     }
 
+    LA_STAMP(7);
     wait_vm<0>();  // the last iteration's copies (of a tile past the segment) have landed
     // ---- segment end: l over both lane halves; write the slot ----
     // This wave holds the pair's 64 heads (own: acc[0..7], partner:
@@ -1387,6 +1426,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     // per lane) and stores them: every store instruction writes eight full
     // 128-B lines.
     lds_barrier();  // every wave has finished with the tile buffers
+    LA_STAMP(8);
     const uint32_t sbase = kStageBytes * wave;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
@@ -1448,9 +1488,16 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         });
       }
     }
+    LA_STAMP(9);
     lo = seg_hi;
     ++s;
   }
+#ifdef LA_PHASE_STAMPS
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  LA_STAMP(10);
+  if ((threadIdx.x & 63) == 0 && blockIdx.x < kStampBlocks)
+    for (int i = 0; i < 11; ++i) g_attn_stamps[((size_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kStampSlots + i] = stamps_[i];
+#endif
 }
 
 // Copies-only variant of the attention kernel, for measuring the streaming
@@ -1663,4 +1710,16 @@ hipError_t launch_decode_mfma(const DecodeProblem& p, hipStream_t stream, hipEve
   return launch_t<__half, false>(p, stream, ev_begin, ev_end);
 }
 
+#ifdef LA_PHASE_STAMPS
+// Phase-timing build: copies (clear == 0) the attention kernel's stamps of
+// blocks 0 .. blocks-1 (4 waves x 12 slots each) to host, or zeroes them.
+extern "C" int la_phase_attn_stamps(unsigned long long* host, int blocks, int clear) {
+  const size_t n = sizeof(unsigned long long) * 4 * kStampSlots * (size_t)(blocks < kStampBlocks ? blocks : kStampBlocks);
+  if (clear) {
+    static unsigned long long zeros[kStampBlocks * 4 * kStampSlots];
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_attn_stamps), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+  }
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_attn_stamps), n, 0, hipMemcpyDeviceToHost);
+}
+#endif
 }  // namespace la

@@ -31,6 +31,37 @@
 #include <type_traits>
 
 namespace la {
+
+// Phase-timing build only (-DLA_PHASE_STAMPS, see la_mfma.hip): wave 0 of
+// every block of the absorb and merge + projection kernels records the
+// device's constant-rate clock (s_memrealtime, 100 MHz, common to all XCDs)
+// at 6 points and writes them at exit. Absorb: 0 entry, 1 loads issued, 2
+// operands in LDS, 3 past the barrier, 4 MFMAs done, 5 stores complete.
+// Merge: 0 entry, 1 W_UV loads issued, 2 this wave's merge done, 3 every
+// wave's merge in LDS, 4 projection done, 5 stores complete.
+#ifdef LA_PHASE_STAMPS
+constexpr int kSideStampBlocks = 8192;
+__device__ unsigned long long g_side_stamps[2][kSideStampBlocks * 8];
+#define LA_RSTAMP(i)                                                               \
+  do {                                                                             \
+    unsigned long long t_;                                                         \
+    asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t_)::"memory"); \
+    stamps_[i] = t_;                                                               \
+  } while (0)
+#define LA_RSTAMP_DECL unsigned long long stamps_[8] = {}
+#define LA_RSTAMP_WRITE(kind)                                                                            \
+  do {                                                                                                   \
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");                                                     \
+    LA_RSTAMP(5);                                                                                        \
+    if (threadIdx.x == 0 && blockIdx.x < kSideStampBlocks)                                               \
+      for (int i_ = 0; i_ < 6; ++i_) g_side_stamps[kind][(size_t)blockIdx.x * 8 + i_] = stamps_[i_];     \
+  } while (0)
+#else
+#define LA_RSTAMP(i) ((void)0)
+#define LA_RSTAMP_DECL ((void)0)
+#define LA_RSTAMP_WRITE(kind) ((void)0)
+#endif
+
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -99,6 +130,8 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
                                                           float* __restrict__ zero_out, int64_t zero_n) {
   typedef Mma<WT> M;
   typedef typename M::vec vec;
+  LA_RSTAMP_DECL;
+  LA_RSTAMP(0);
   // both 64-B scalar-cache lines of the arguments in one round of loads (see
   // warm_kernarg_lines)
   asm volatile("" ::"s"(tokens), "s"(qps));
@@ -152,6 +185,7 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
     if (NKS > 0 ? k < NKS : q < dn * 16)
       wv[k] = *reinterpret_cast<const i16x8*>(W + ((int64_t)h * dn + (q >> 4)) * dc + cb * kAbsCols + (q & 15) * 8);
   }
+  LA_RSTAMP(1);
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const int q = tid + 256 * k;
@@ -173,7 +207,9 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
       *reinterpret_cast<vec*>(qs + (2 * ks + 1) * 1024 + 16 * lane) = lo;
     }
   }
+  LA_RSTAMP(2);
   __syncthreads();
+  LA_RSTAMP(3);
 
   f32x16 acc_hi = {}, acc_lo = {};
   const int g = lane >> 4, s = lane & 15;
@@ -199,6 +235,7 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
     acc_hi = M::mma(b, ahi, acc_hi);
     acc_lo = M::mma(b, alo, acc_lo);
   }
+  LA_RSTAMP(4);
   // D^T[m = column][n = token]: register 4q + r holds column 32w + 8q + 4(lane/32) + r
   // of token t0 + lane%32, so one 16-byte (fp32) or 8-byte (16-bit) store per q.
   const int tt = t0 + (lane & 31);
@@ -257,6 +294,7 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
       }
     }
   }
+  LA_RSTAMP_WRITE(0);
 }
 
 // ---------------------------------------------------------------------------
@@ -478,6 +516,8 @@ constexpr int kMPOPitch = kDcP + 8;
 
 template <typename WT, bool F16>
 __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProblem p) {
+  LA_RSTAMP_DECL;
+  LA_RSTAMP(0);
   warm_kernarg_lines(p);
   typedef Mma16<WT> M;
   typedef typename M::vec vec;
@@ -500,6 +540,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
   vec bw[16];
 #pragma unroll
   for (int ks = 0; ks < 16; ++ks) bw[ks] = __builtin_bit_cast(vec, *reinterpret_cast<const i16x8*>(wrow + 32 * ks));
+  LA_RSTAMP(1);
 
   // row r, columns c0 .. c0 + 7 of O -> high and low operand rows
   auto put8 = [&](int r, int c0, const float (&v)[8]) {
@@ -512,6 +553,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
   if (rows >= kMPWaves) {
     const int t[2] = {rb * kMPRows + wave, wave + kMPWaves < rows ? rb * kMPRows + wave + kMPWaves : -1};
     merge_tasks<F16>(p, t, h, 0, 1, lane, o);
+    LA_RSTAMP(2);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const bool live = q == 0 || t[1] >= 0;
@@ -529,6 +571,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
     const int r = wave / G, g = wave % G;
     const int t[2] = {r < rows ? rb * kMPRows + r : -1, -1};
     merge_tasks<F16>(p, t, h, g, G, lane, o);
+    LA_RSTAMP(2);
     *reinterpret_cast<f32x4*>(&gp[wave * kMPPitch + 8 * lane]) = o[0][0];
     *reinterpret_cast<f32x4*>(&gp[wave * kMPPitch + 8 * lane + 4]) = o[0][1];
     __syncthreads();
@@ -554,6 +597,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
   }
 
   // A[m = lane % 16][k = 32 ks + 8 (lane / 16) + j] = O[m][k] (high, low)
+  LA_RSTAMP(3);
   f32x4 acc_hi = {}, acc_lo = {};
   const int a0 = (lane & 15) * kMPOPitch + 8 * (lane >> 4);
 #pragma unroll
@@ -563,6 +607,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
     acc_hi = M::mma(hi, bw[ks], acc_hi);
     acc_lo = M::mma(lo, bw[ks], acc_lo);
   }
+  LA_RSTAMP(4);
   // D[m = 4 (lane / 16) + i][n = lane % 16]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -573,6 +618,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
       p.out[orow * p.dv + 16 * wave + (lane & 15)] = acc_hi[i] + acc_lo[i] * (1.f / kLoScale);
     }
   }
+  LA_RSTAMP_WRITE(1);
 }
 
 // Merge + W_UV projection over one latent half, for launches with fewer
@@ -590,6 +636,8 @@ constexpr int kMPHSum = 256 + 4;    // floats per LDS row of a slot-group sum
 
 template <typename WT>
 __global__ __launch_bounds__(kMPWaves * 64) void merge_project_half_kernel(DecodeProblem p) {
+  LA_RSTAMP_DECL;
+  LA_RSTAMP(0);
   warm_kernarg_lines(p);
   typedef Mma16<WT> M;
   typedef typename M::vec vec;
@@ -617,6 +665,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_half_kernel(Decod
   vec bw[8];
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) bw[ks] = __builtin_bit_cast(vec, *reinterpret_cast<const i16x8*>(wrow + 32 * ks));
+  LA_RSTAMP(1);
 
   // row r, columns c0 .. c0 + 3 of the half -> high and low operand rows
   auto put4 = [&](int r, int c0, const f32x4& v) {
@@ -634,6 +683,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_half_kernel(Decod
   if (rows >= kMPWaves) {
     const int t[2] = {rb * kMPRows + wave, wave + kMPWaves < rows ? rb * kMPRows + wave + kMPWaves : -1};
     merge_tasks<true, true>(p, t, h, 0, 1, lane, o, c);
+    LA_RSTAMP(2);
     put4(wave, 4 * lane, o[0][0]);
     put4(wave + kMPWaves, 4 * lane, t[1] >= 0 ? o[1][0] : f32x4{0.f, 0.f, 0.f, 0.f});
     __syncthreads();
@@ -642,6 +692,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_half_kernel(Decod
     const int r = wave / G, g = wave % G;
     const int t[2] = {r < rows ? rb * kMPRows + r : -1, -1};
     merge_tasks<true, true>(p, t, h, g, G, lane, o, c);
+    LA_RSTAMP(2);
     *reinterpret_cast<f32x4*>(&gp[wave * kMPHSum + 4 * lane]) = o[0][0];
     __syncthreads();
     // O half row r = sum of the G group rows of waves r G .. r G + G - 1; the
@@ -657,6 +708,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_half_kernel(Decod
   }
 
   // A[m = lane % 16][k = 32 ks + 8 (lane / 16) + j] = O[m][256 c + k] (high, low)
+  LA_RSTAMP(3);
   f32x4 acc_hi = {}, acc_lo = {};
   const int a0 = (lane & 15) * kMPHPitch + 8 * (lane >> 4);
 #pragma unroll
@@ -666,6 +718,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_half_kernel(Decod
     acc_hi = M::mma(hi, bw[ks], acc_hi);
     acc_lo = M::mma(lo, bw[ks], acc_lo);
   }
+  LA_RSTAMP(4);
   // D[m = 4 (lane / 16) + i][n = lane % 16], added into the zeroed output
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -676,6 +729,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_half_kernel(Decod
       atomicAdd(&p.out[orow * p.dv + 16 * wave + (lane & 15)], acc_hi[i] + acc_lo[i] * (1.f / kLoScale));
     }
   }
+  LA_RSTAMP_WRITE(1);
 }
 
 }  // namespace
@@ -746,4 +800,19 @@ hipError_t launch_combine_project_mfma(const DecodeProblem& p, hipStream_t strea
   return hipGetLastError();
 }
 
+#ifdef LA_PHASE_STAMPS
+// Phase-timing build: copies (clear == 0) the stamps of kernel kind (0
+// absorb, 1 merge + projection) of blocks 0 .. blocks-1 (8 slots each) to
+// host, or zeroes them.
+extern "C" int la_phase_side_stamps(int kind, unsigned long long* host, int blocks, int clear) {
+  if (kind < 0 || kind > 1) return (int)hipErrorInvalidValue;
+  const size_t one = sizeof(unsigned long long) * 8 * kSideStampBlocks;
+  if (clear) {
+    static unsigned long long zeros[kSideStampBlocks * 8];
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_side_stamps), zeros, one, one * kind, hipMemcpyHostToDevice);
+  }
+  const size_t n = sizeof(unsigned long long) * 8 * (size_t)(blocks < kSideStampBlocks ? blocks : kSideStampBlocks);
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_side_stamps), n, one * kind, hipMemcpyDeviceToHost);
+}
+#endif
 }  // namespace la
