@@ -397,17 +397,13 @@ template <typename T>
 __device__ inline void lds_st(lchar* L, uint32_t off, T v) {
   *reinterpret_cast<__attribute__((address_space(3))) T*>(L + off) = v;
 }
-// 16-B global store at device scope (sc1): written through this XCD's L2 to
-// the device's coherence point. The partial slots go out this way, so the
-// release at the end of the grid finds no dirty partial lines left in the L2s
-// to write back (attention -2 us at config 3), and the merge kernel, on any
-// XCD, still reads them from the infinity cache (its time is unchanged).
-__device__ inline void st_global_dev16(void* p, i16x8 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
-}
-// The same policy on buffer stores (the cache-policy operand's sc1 bit), and
-// word 3 of a raw buffer resource (32-bit data format, as the gfx9 family
-// expects).
+// Partial-slot stores go out at device scope: the cache-policy operand's sc1
+// bit on a buffer store writes through this XCD's L2 to the device's
+// coherence point, so the release at the end of the grid finds no dirty
+// partial lines left in the L2s to write back (attention -2 us at config 3),
+// and the merge kernel, on any XCD, still reads them from the infinity cache
+// (its time is unchanged). kBufferRsrcWord3 is word 3 of a raw buffer
+// resource (32-bit data format, as the gfx9 family expects).
 constexpr int kCpolSc1 = 16;
 constexpr int kBufferRsrcWord3 = 0x00020000;
 // ds_read_b64_tr_b16 as inline asm: the builtin makes the compiler assume the
@@ -1428,8 +1424,10 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     lds_barrier();  // every wave has finished with the tile buffers
     LA_STAMP(8);
     const uint32_t sbase = kStageBytes * wave;
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    // stage(b): half rows b (0: own heads, staged rows 0..31; 1: the
+    // partner's, rows 32..63), one 16-column block at a time
+    auto stage = [&](auto b_c) {
+      constexpr int b = decltype(b_c)::value;
 #pragma unroll
       for (int cb = 0; cb < 8; ++cb) {
         const f32x16 v = acc[8 * b + cb] * (b == 0 ? mulo : mulp);
@@ -1442,52 +1440,65 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes before its reads
-    {
-      const int lr = lane_id();  // fresh index: values derived earlier would come back from spill slots
-      const uint32_t rd = sbase + (lr >> 5) * kStagePitch + 16 * (lr & 31);
-      _Float16* const obase = reinterpret_cast<_Float16*>(p.part_o) + hqg * kDc + 256 * ch + 8 * (lr & 31);
-      // all 32 reads in flight (each round in its own registers, so no store
-      // source is overwritten while the store may still read it), one wait,
-      // then the 32 stores back to back
-      i16x8 xr[32];
-      static_for<32>([&](auto j_c) {
+    };
+    const int lr = lane_id();  // fresh index: values derived earlier would come back from spill slots
+    const uint32_t rd = sbase + (lr >> 5) * kStagePitch + 16 * (lr & 31);
+    // read16(h, x): staged rows 32h + 2j (lanes 0..31) and 32h + 2j + 1
+    // (lanes 32..63), j < 16, 16 B per lane
+    auto read16 = [&](auto h_c, i16x8(&x)[16]) {
+      constexpr int h = decltype(h_c)::value;
+      static_for<16>([&](auto j_c) {
         constexpr int j = decltype(j_c)::value;
-        xr[j] = lds_rd128<i16x8, 2 * kStagePitch * j>(L, rd);
+        x[j] = lds_rd128<i16x8, 2 * kStagePitch * (16 * h + j)>(L, rd);
       });
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xr[0]), "+v"(xr[1]), "+v"(xr[2]), "+v"(xr[3]), "+v"(xr[4]), "+v"(xr[5]), "+v"(xr[6]), "+v"(xr[7]));
-      // the wait above covers every read: the rest are ties only
-      asm volatile("" : "+v"(xr[8]), "+v"(xr[9]), "+v"(xr[10]), "+v"(xr[11]), "+v"(xr[12]), "+v"(xr[13]), "+v"(xr[14]), "+v"(xr[15]));
-      asm volatile("" : "+v"(xr[16]), "+v"(xr[17]), "+v"(xr[18]), "+v"(xr[19]), "+v"(xr[20]), "+v"(xr[21]), "+v"(xr[22]), "+v"(xr[23]));
-      asm volatile("" : "+v"(xr[24]), "+v"(xr[25]), "+v"(xr[26]), "+v"(xr[27]), "+v"(xr[28]), "+v"(xr[29]), "+v"(xr[30]), "+v"(xr[31]));
+    };
+    // The slot rows of this group in one raw buffer that ends at its last
+    // valid head row, so a store of a row past it is dropped by the range
+    // check (raw buffer stores outside num_records write nothing). A full
+    // group (every benchmark shape) puts the row in the scalar offset: one
+    // scalar add per store, no exec mask and no vector address arithmetic;
+    // a partial one puts it in the vector offset, which the range check sees.
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<_Float16*>(p.part_o) + hqg * kDc, 0, hg_heads * kDc * 2, kBufferRsrcWord3);
+    const int vlane = (lr >> 5) * (kDc * 2) + 512 * ch + 16 * (lr & 31);
+    // row offsets of staged rows 0 and 32, made here (the empty asm) so the
+    // per-store offsets below are one add each rather than 32 values
+    // computed at kernel start and held in spill slots
+    int own = 32 * wave * (kDc * 2), par = 32 * pw * (kDc * 2);
+    asm volatile("" : "+s"(own), "+s"(par));
+    auto store16 = [&](const int rows, const i16x8(&x)[16]) {
       if (hg_heads == kHG) {
-        // a full group (every benchmark shape): no row to mask, so each
-        // store is the lane offset plus a wave-uniform row offset in an
-        // SGPR, with no per-store exec mask or address arithmetic
-        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-            reinterpret_cast<_Float16*>(p.part_o) + hqg * kDc, 0, kHG * kDc * 2, kBufferRsrcWord3);
-        const int vlane = (lr >> 5) * (kDc * 2) + 512 * ch + 16 * (lr & 31);
-        // row offsets of staged rows 0 and 32 (own heads, then the
-        // partner's), made here (the empty asm) so the per-store offsets
-        // below are one scalar add each rather than 32 values computed at
-        // kernel start and held in spill slots
-        int own = 32 * wave * (kDc * 2), par = 32 * pw * (kDc * 2);
-        asm volatile("" : "+s"(own), "+s"(par));
-        static_for<32>([&](auto j_c) {
+        static_for<16>([&](auto j_c) {
           constexpr int j = decltype(j_c)::value;
-          const int soff = j < 16 ? own + 2 * j * (kDc * 2) : par + 2 * (j - 16) * (kDc * 2);  // staged rows 2j, 2j+1
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xr[j]), rsrc, vlane, soff, kCpolSc1);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x[j]), rsrc, vlane, rows + 2 * j * (kDc * 2),
+                                                 kCpolSc1);
         });
       } else {
-        static_for<32>([&](auto j_c) {
+        static_for<16>([&](auto j_c) {
           constexpr int j = decltype(j_c)::value;
-          const int r = 2 * j + (lr >> 5);                             // staged row
-          const int hb = r < 32 ? 32 * wave + r : 32 * pw + (r - 32);  // head within the group
-          if (hb < hg_heads) st_global_dev16(obase + (uint32_t)(hb * kDc), xr[j]);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x[j]), rsrc, vlane + rows + 2 * j * (kDc * 2),
+                                                 0, kCpolSc1);
         });
       }
-    }
+    };
+    // Two halves, so each half's LDS reads and stores overlap other work:
+    // the own half rows' reads run while the partner's are converted and
+    // staged, and their stores while the partner's reads run. Each read
+    // lands in its own registers, held (the empty asm ties) until the
+    // lgkmcnt(0) that covers it.
+    stage(std::integral_constant<int, 0>());
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's own-half writes before their reads
+    i16x8 xa[16];
+    read16(std::integral_constant<int, 0>(), xa);
+    stage(std::integral_constant<int, 1>());
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xa[0]), "+v"(xa[1]), "+v"(xa[2]), "+v"(xa[3]), "+v"(xa[4]), "+v"(xa[5]), "+v"(xa[6]), "+v"(xa[7]));
+    asm volatile("" : "+v"(xa[8]), "+v"(xa[9]), "+v"(xa[10]), "+v"(xa[11]), "+v"(xa[12]), "+v"(xa[13]), "+v"(xa[14]), "+v"(xa[15]));
+    store16(own, xa);
+    i16x8 xb[16];
+    read16(std::integral_constant<int, 1>(), xb);  // the partner half's writes completed at the wait above
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xb[0]), "+v"(xb[1]), "+v"(xb[2]), "+v"(xb[3]), "+v"(xb[4]), "+v"(xb[5]), "+v"(xb[6]), "+v"(xb[7]));
+    asm volatile("" : "+v"(xb[8]), "+v"(xb[9]), "+v"(xb[10]), "+v"(xb[11]), "+v"(xb[12]), "+v"(xb[13]), "+v"(xb[14]), "+v"(xb[15]));
+    store16(par, xb);
     LA_STAMP(9);
     lo = seg_hi;
     ++s;
