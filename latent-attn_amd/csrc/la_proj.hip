@@ -185,6 +185,18 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
     if (NKS > 0 ? k < NKS : q < dn * 16)
       wv[k] = *reinterpret_cast<const i16x8*>(W + ((int64_t)h * dn + (q >> 4)) * dc + cb * kAbsCols + (q & 15) * 8);
   }
+  // q_rope rows of the block's tokens for the q_prep rows' rope part, written
+  // by the column block 0 of each head: 32 tokens x 64 = one 32-B piece per
+  // thread (dc + dR = 576 on this path, so dR = 64). Loaded here with the
+  // operands, so the tail after the MFMAs is one store, not a load round
+  // trip; by every block (the other column blocks of the head read the same
+  // lines from the XCD's L2) and unconditionally (without q_rope, out_mode 0,
+  // from q_nope instead, unused), since a load under a branch gets its result
+  // copied at the branch's end, which would wait for every load before it.
+  const int rtr = min(t0 + (tid >> 3), tokens - 1);
+  const float* rsrc = out_mode != 0 ? q_rope + ((int64_t)rtr * nh + h) * dR + 8 * (tid & 7) : q_nope;
+  const f32x4 ra = *reinterpret_cast<const f32x4*>(rsrc);
+  const f32x4 rb = *reinterpret_cast<const f32x4*>(rsrc + 4);
   LA_RSTAMP(1);
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
@@ -264,31 +276,27 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
       }
     }
   }
-  const int hq_pad = out_mode != 0 ? qprep_rows_per_seq(qps * nh) : 0;
-  auto qrow_of = [&](int t) -> int64_t { return (int64_t)(t / qps) * hq_pad + (int64_t)(t % qps) * nh + h; };
   if (out_mode != 0 && cb == 0) {
-    // q_rope part of the same rows: 8 elements (one 16-B slot of q_prep) per thread-step
-    for (int q = tid; q < 32 * (dR / 8); q += 256) {
-      const int tr = t0 + q / (dR / 8), j = 8 * (q % (dR / 8));
-      if (tr >= tokens) continue;
-      const int64_t row = (int64_t)tr * nh + h;
-      const f32x4 a = *reinterpret_cast<const f32x4*>(q_rope + row * dR + j);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(q_rope + row * dR + j + 4);
-      const int64_t dst = qprep_index(qrow_of(tr), dc + j);
+    // the q_rope part of the same rows (loaded with the operands above): one
+    // 16-B slot of q_prep per thread
+    const int tr = t0 + (tid >> 3), j = 8 * (tid & 7);
+    if (tr < tokens) {
+      const int64_t qr = (int64_t)(tr / qps) * qprep_rows_per_seq(qps * nh) + (int64_t)(tr % qps) * nh + h;
+      const int64_t dst = qprep_index(qr, dc + j);
       if (out_mode == 1) {
         bf16x8 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[e] = (__bf16)(a[e] * scale);
-          v[4 + e] = (__bf16)(b[e] * scale);
+          v[e] = (__bf16)(ra[e] * scale);
+          v[4 + e] = (__bf16)(rb[e] * scale);
         }
         *reinterpret_cast<bf16x8*>(reinterpret_cast<__bf16*>(out) + dst) = v;
       } else {
         f16x8 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[e] = (_Float16)(a[e] * scale);
-          v[4 + e] = (_Float16)(b[e] * scale);
+          v[e] = (_Float16)(ra[e] * scale);
+          v[4 + e] = (_Float16)(rb[e] * scale);
         }
         *reinterpret_cast<f16x8*>(reinterpret_cast<_Float16*>(out) + dst) = v;
       }
