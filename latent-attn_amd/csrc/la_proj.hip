@@ -404,31 +404,32 @@ __device__ inline MergeTask merge_task(const DecodeProblem& p, int t, int h, int
 }
 
 // Merges up to two tasks (t[1] < 0: one) of the same slot group g of G.
-// Every load of both tasks goes out before anything waits: the first 8 slot
+// Every load of both tasks goes out before anything waits: the first NB slot
 // rows of each task, each row's log-sum-exps (lane i: slot i, for the
 // maximum and the denominator) and the weights' inputs of the task's own
-// slots (lane i: slot g + G i), so a merge of up to 8 own slots out of at
+// slots (lane i: slot g + G i), so a merge of up to NB own slots out of at
 // most 64 takes one memory round trip. Longer merges loop over further
-// groups of 8 rows (and of 64 slots). Lane i's weights are broadcast with
+// groups of NB rows (and of 64 slots). Lane i's weights are broadcast with
 // v_readlane.
 // kHalf: half-row merge of latent half c (o[k][1] stays 0).
-template <bool F16, bool kHalf = false>
+template <bool F16, bool kHalf, int NB>
 __device__ inline void merge_tasks(const DecodeProblem& p, const int (&t)[2], int h, int g, int G, int lane,
                                    f32x4 (&o)[2][2], int c = 0) {
   static_assert(F16 || !kHalf, "half-row merges read fp16 slots");
   typedef typename std::conditional<F16, _Float16, float>::type PT;
   typedef typename std::conditional<kHalf, SlotRowHalf, SlotRow<F16>>::type SR;
   const int64_t sstride = (int64_t)p.Hq * kDcP;
+  static_assert(NB >= 1 && NB <= 64, "slot rows per batch");
   MergeTask mt[2];
   const PT* src[2];
-  SR d[2][8];
+  SR d[2][NB];
   float ls_all[2], ls_own[2], m_own[2], sa_own[2], sb_own[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     mt[k] = merge_task(p, t[k], h, g, G);
     src[k] = reinterpret_cast<const PT*>(p.part_o) + mt[k].row0 * kDcP + (kHalf ? 256 * c + 4 * lane : 8 * lane);
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < NB; ++u)
       if (u < mt[k].ns) d[k][u].load(src[k] + (int64_t)(g + G * u) * sstride);
   }
 #pragma unroll
@@ -480,14 +481,14 @@ __device__ inline void merge_tasks(const DecodeProblem& p, const int (&t)[2], in
       } else {
         wlo = whi = exp2f(ls - mx) * inv;
       }
-      for (int j = 0; j < nb; j += 8) {
+      for (int j = 0; j < nb; j += NB) {
         if (i0 > 0 || j > 0) {
 #pragma unroll
-          for (int u = 0; u < 8; ++u)
+          for (int u = 0; u < NB; ++u)
             if (j + u < nb) d[k][u].load(src[k] + (int64_t)(g + G * (i0 + j + u)) * sstride);
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < NB; ++u) {
           if (j + u < nb) {
             const float w0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wlo), j + u));
             const float w1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, whi), j + u));
@@ -516,6 +517,12 @@ __device__ inline void merge_tasks(const DecodeProblem& p, const int (&t)[2], in
 // Blocks of one head run on one XCD (the dispatcher assigns id % 8 to XCDs),
 // so its 128 KB of W_UV is fetched once per head.
 constexpr int kMPWaves = 8;
+// slot rows each task loads up front (one memory round trip for up to this
+// many; more loop over further batches, a round trip each). The half-row
+// merge also comes with 32 (8 B per lane each), launched when a task has
+// more than 8 slots (config 5: 32): more registers cost the short merges
+// (measured: configs 2 and 3 +1.5 us per step with 16 / 32 everywhere).
+constexpr int kMPSlots = 8;
 constexpr int kMPPitch = kDcP + 4;  // floats per LDS row of a slot-group sum
 // 16-bit elements per LDS row of the high / low operand rows: 1040 B, 16 B
 // past a multiple of 256, so the 16 rows one A read touches (16 lanes, one
@@ -560,7 +567,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
   f32x4 o[2][2];
   if (rows >= kMPWaves) {
     const int t[2] = {rb * kMPRows + wave, wave + kMPWaves < rows ? rb * kMPRows + wave + kMPWaves : -1};
-    merge_tasks<F16>(p, t, h, 0, 1, lane, o);
+    merge_tasks<F16, false, kMPSlots>(p, t, h, 0, 1, lane, o);
     LA_RSTAMP(2);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -578,7 +585,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
     const int G = kMPWaves / rows;
     const int r = wave / G, g = wave % G;
     const int t[2] = {r < rows ? rb * kMPRows + r : -1, -1};
-    merge_tasks<F16>(p, t, h, g, G, lane, o);
+    merge_tasks<F16, false, kMPSlots>(p, t, h, g, G, lane, o);
     LA_RSTAMP(2);
     *reinterpret_cast<f32x4*>(&gp[wave * kMPPitch + 8 * lane]) = o[0][0];
     *reinterpret_cast<f32x4*>(&gp[wave * kMPPitch + 8 * lane + 4]) = o[0][1];
@@ -642,7 +649,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_kernel(DecodeProb
 constexpr int kMPHPitch = 256 + 8;  // 16-bit elements per LDS operand row (528 B: 16 B past 2 x 256)
 constexpr int kMPHSum = 256 + 4;    // floats per LDS row of a slot-group sum
 
-template <typename WT>
+template <typename WT, int NB>
 __global__ __launch_bounds__(kMPWaves * 64) void merge_project_half_kernel(DecodeProblem p) {
   LA_RSTAMP_DECL;
   LA_RSTAMP(0);
@@ -690,7 +697,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_half_kernel(Decod
   f32x4 o[2][2];
   if (rows >= kMPWaves) {
     const int t[2] = {rb * kMPRows + wave, wave + kMPWaves < rows ? rb * kMPRows + wave + kMPWaves : -1};
-    merge_tasks<true, true>(p, t, h, 0, 1, lane, o, c);
+    merge_tasks<true, true, NB>(p, t, h, 0, 1, lane, o, c);
     LA_RSTAMP(2);
     put4(wave, 4 * lane, o[0][0]);
     put4(wave + kMPWaves, 4 * lane, t[1] >= 0 ? o[1][0] : f32x4{0.f, 0.f, 0.f, 0.f});
@@ -699,7 +706,7 @@ __global__ __launch_bounds__(kMPWaves * 64) void merge_project_half_kernel(Decod
     const int G = kMPWaves / rows;
     const int r = wave / G, g = wave % G;
     const int t[2] = {r < rows ? rb * kMPRows + r : -1, -1};
-    merge_tasks<true, true>(p, t, h, g, G, lane, o, c);
+    merge_tasks<true, true, NB>(p, t, h, g, G, lane, o, c);
     LA_RSTAMP(2);
     *reinterpret_cast<f32x4*>(&gp[wave * kMPHSum + 4 * lane]) = o[0][0];
     __syncthreads();
@@ -786,10 +793,20 @@ hipError_t launch_combine_project_mfma(const DecodeProblem& p, hipStream_t strea
     if (!p.part_f16) return hipErrorInvalidValue;
     // id = 8 (2 (head / 8 * nrb + row block) + half) + head % 8
     const dim3 grid((unsigned)(2 * merge_project_blocks(p)));
-    if (p.wuv_dtype == LA_DTYPE_BF16)
-      hipLaunchKernelGGL(merge_project_half_kernel<__hip_bfloat16>, grid, dim3(kMPWaves * 64), 0, stream, p);
-    else
-      hipLaunchKernelGGL(merge_project_half_kernel<__half>, grid, dim3(kMPWaves * 64), 0, stream, p);
+    // slots per task with equal sequences (seq_len / chunk_len when chunks
+    // align with the sequences, else up to two more; rows of a block share
+    // G = 8 / rows tasks); ragged or capacity caches keep the 8-slot batches
+    const int rows = R < kMPRows ? R : kMPRows;
+    const int G = rows >= kMPWaves ? 1 : kMPWaves / rows;
+    const int64_t n = p.offsets || p.lens || p.chunk_len <= 0 ? 0
+                      : p.seq_len % p.chunk_len == 0 ? p.seq_len / p.chunk_len
+                                                     : p.seq_len / p.chunk_len + 2;
+    const bool wide = (n + G - 1) / G > kMPSlots;
+    auto k = p.wuv_dtype == LA_DTYPE_BF16 ? (wide ? merge_project_half_kernel<__hip_bfloat16, 32>
+                                                  : merge_project_half_kernel<__hip_bfloat16, kMPSlots>)
+                                          : (wide ? merge_project_half_kernel<__half, 32>
+                                                  : merge_project_half_kernel<__half, kMPSlots>);
+    hipLaunchKernelGGL(k, grid, dim3(kMPWaves * 64), 0, stream, p);
     return hipGetLastError();
   }
   // id = 8 (head / 8 * nrb + row block) + head % 8
