@@ -1040,6 +1040,18 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         if (lz < 40) lds_st(L, kAtabOff + par * kAtabPar + wave * kAtabWave + 4 * lz, 0.f);
       }
     }
+    // lane parts of the loop's LDS addresses (the buffer offsets are
+    // per-iteration scalars added to them)
+    int lct, lrp, ltb0, ltb1;
+    {
+      const int ln = lane_id();
+      const int ar = ln & 31, gg = ln >> 5, q16 = ln >> 4, s16 = ln & 15;
+      lct = ct_row_off(ar) + 16 * gg;
+      lrp = ar * 128 + 16 * (gg ^ fr(ar));
+      const int tc = 32 * (q16 & 1) + 8 * (s16 & 3) + 512 * ch;
+      ltb0 = tc + ct_row_off(4 * (q16 >> 1) + (s16 >> 2));
+      ltb1 = tc + ct_row_off(8 + 4 * (q16 >> 1) + (s16 >> 2));
+    }
     for (int t = -1; t < ntiles; ++t) {
 #ifdef LA_PHASE_STAMPS
       if (t == 0) LA_STAMP(6);
@@ -1088,8 +1100,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // read kQkDepth k-steps ahead of their MFMA. The last iteration skips
       // the phase (no tile t+1).
       const int arow = lane & 31;
-      const uint32_t ct_x = nxt + ct_row_off(arow) + 16 * g2;
-      const uint32_t rp_x = (nxt + kRopeOff + arow * 128) | (16 * (g2 ^ fr(arow)));
+      const uint32_t ct_x = nxt + lct;
+      const uint32_t rp_x = nxt + kRopeOff + lrp;  // nxt + kRopeOff is a multiple of 128
       const uint32_t pp_x = kPtabOff + par * kPtabPar + pw * 2048 + 16 * lane;
       // paged: this iteration's copies use tile t+2's entry (loaded in the
       // previous iteration or the prologue); tile t+3's goes out now and is
@@ -1109,9 +1121,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // ct_row_off(rho) = 16ks kRowPitch + ct_row_off(rho - 16ks), so read x
       // is lane base tb_x plus the immediate 16ks kRowPitch + 64nb; this
       // wave's column blocks are nb = 8ch + cb.
-      const uint32_t tcol = cur + 32 * (q16 & 1) + 8 * (s16 & 3) + 512 * ch;
-      const uint32_t tb0 = tcol + ct_row_off(4 * (q16 >> 1) + (s16 >> 2));
-      const uint32_t tb1 = tcol + ct_row_off(8 + 4 * (q16 >> 1) + (s16 >> 2));
+      const uint32_t tb0 = cur + ltb0;
+      const uint32_t tb1 = cur + ltb1;
       TrPair tr[kPvDepth];
       auto b_issue = [&](TrPair& r, auto step_c) {
         constexpr int step = decltype(step_c)::value;
