@@ -880,12 +880,28 @@ static_assert(fp8_half_order_ok(), "fp8 expansion halves overlap");
 __host__ __device__ inline int64_t mfma_grid_blocks(int num_chunks, int groups) {
   return 8 * (((int64_t)num_chunks * groups + 7) / 8);
 }
+// 32-bit arithmetic: the grid (8 per blocks) is below 2^31, so every item
+// is (a 64-bit division here is ~130 dependent scalar instructions at the
+// kernel's start).
 __device__ inline void block_coords(int num_chunks, int groups, int* chunk, int* group) {
-  const int id = blockIdx.x;
-  const int64_t per = ((int64_t)num_chunks * groups + 7) / 8;
-  const int64_t item = (id & 7) * per + (id >> 3);
-  *group = (int)(item % groups);
-  *chunk = (int)(item / groups);
+  const uint32_t id = blockIdx.x;
+  const uint32_t per = ((uint32_t)num_chunks * (uint32_t)groups + 7) / 8;
+  const uint32_t item = (id & 7) * per + (id >> 3);
+  if (groups == 1) {
+    *group = 0;
+    *chunk = (int)item;
+  } else {
+    const uint32_t c = item / (uint32_t)groups;
+    *group = (int)(item - c * (uint32_t)groups);
+    *chunk = (int)c;
+  }
+}
+
+// find_seq for the MFMA kernels: with uniform sequences the row space is
+// below 2^31 rows (mfma_supported), so the division is a 32-bit one.
+__device__ inline int find_seq_mfma(const DecodeProblem& p, int64_t r) {
+  if (p.offsets) return find_seq(p, r);
+  return (int)((uint32_t)r / (uint32_t)p.seq_len);
 }
 
 // kFp8: FP8 E4M3 cache rows (KT = bf16: the tiles are expanded to bf16 in
@@ -917,7 +933,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
   const int64_t hi = min(lo + (int64_t)p.chunk_len, end_all);
   lo = max(lo, seq_begin(p, 0));
   if (lo >= hi) return;
-  int s = find_seq(p, lo);
+  int s = find_seq_mfma(p, lo);
 
   while (lo < hi) {
     const int64_t s_lo = seq_begin(p, s);
@@ -1547,7 +1563,7 @@ __global__ __launch_bounds__(kThreads) void stream_copies_kernel(DecodeProblem p
   const int64_t hi = min(lo + (int64_t)p.chunk_len, end_all);
   lo = max(lo, seq_begin(p, 0));
   if (lo >= hi) return;
-  int s = find_seq(p, lo);
+  int s = find_seq_mfma(p, lo);
   while (lo < hi) {
     const int64_t s_lo = seq_begin(p, s);
     lo = max(lo, s_lo);
@@ -1679,6 +1695,9 @@ bool mfma_supported(const DecodeProblem& p) {
   if (p.kv_dtype != LA_DTYPE_BF16 && p.kv_dtype != LA_DTYPE_F16 && p.kv_dtype != LA_DTYPE_FP8_E4M3) return false;
   if (p.dc != kDc || p.dR != kDr || p.Hq % 16 != 0 || p.Hq <= 0) return false;
   if (p.rope_rows > (1 << 24) || (p.rope_rows == 0 && p.total_rows > (1 << 24))) return false;
+  // uniform sequences: row indices fit in 31 bits (find_seq_mfma); offsets
+  // are int32, so they always do
+  if (!p.offsets && (int64_t)p.num_seqs * p.seq_len > INT32_MAX) return false;
   // paged: a 32-row tile must lie inside one block
   if (p.block_table && (p.block_size % kT != 0 || p.chunk_len % kT != 0)) return false;
   // 16-byte aligned cache rows, table rows and query rows
