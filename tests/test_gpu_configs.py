@@ -254,6 +254,29 @@ def test_mfma_plan_for_the_shared_cache_entry(cuda, abi, batch, seq_len, want):
     assert got == want
 
 
+@pytest.mark.parametrize("seq_len, mfma", [((1 << 30) - 32, True), ((1 << 30) + 32, False)])
+def test_mfma_plan_needs_a_31_bit_uniform_row_space(cuda, abi, seq_len, mfma):
+    """The MFMA kernels find a uniform sequence by a 32-bit division of the
+    row index, so la_mla_decode keeps them to row spaces below 2^31 rows (two
+    sequences of 2^30 - 32 rows: MFMA; of 2^30 + 32: not, the VALU kernel or
+    LA_ERROR_NOT_SUPPORTED). The plan query touches no cache memory."""
+    lib, capi = abi
+    a = capi.DecodeArgs()
+    fake = 0x10000
+    a.kv_cache, a.kv_dtype, a.total_rows, a.num_seqs, a.seq_len = fake, capi.LA_DTYPE_BF16, 2 * seq_len, 2, seq_len
+    a.queries_per_seq, a.q_absorbed, a.q_rope = 1, fake, fake
+    a.W_UV, a.w_uv_dtype, a.rope_cos, a.rope_sin, a.rope_rows, a.output = fake, capi.LA_DTYPE_BF16, fake, fake, 8192, fake
+    from latent_attn import MLAConfig
+    a.cfg = capi.config(MLAConfig.deepseek_v2())
+    info = capi.PlanInfo()
+    st = lib.la_mla_decode_plan(ctypes.byref(a), ctypes.byref(info))
+    print(f"[plan rows={2 * seq_len}] status {st} attention {info.attention}", flush=True)
+    if mfma:
+        assert st == 0 and info.attention == capi.LA_PLAN_ATTENTION_MFMA
+    else:
+        assert st == capi.LA_ERROR_NOT_SUPPORTED or (st == 0 and info.attention != capi.LA_PLAN_ATTENTION_MFMA)
+
+
 def test_config3_batched_uniform(cuda, abi):
     lib, capi = abi
     inp = bench.build_inputs("cfg3", cuda)
