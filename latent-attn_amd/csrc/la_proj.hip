@@ -15,10 +15,11 @@
 // (fp16). For fp16 the residual is pre-multiplied by 2^11 (and its product by
 // 2^-11) so it stays in the normal range.
 //
-// absorb:  one block of 256 threads per (32-token block, head, 128-column
-//          block), XCD-ordered; W_UK[h][:, 128-col block] (128 x 128) is
-//          staged in LDS; wave w owns 32 columns; the B operand (8
-//          consecutive rows i per lane) comes from ds_read_b64_tr_b16.
+// absorb:  one block of 512 threads per (32-token block, head, 128-column
+//          block), XCD-ordered; all 8 waves load W_UK[h][:, 128-col block]
+//          (128 x 128) into LDS and one q k-step each, then waves 0..3 run
+//          the MFMAs, wave w on 32 columns; the B operand (8 consecutive
+//          rows i per lane) comes from ds_read_b64_tr_b16.
 // merge + project: merge_project_kernel, one block of 8 waves per (weight
 //          head, 16 query rows): the log-sum-exp merge of the partial slots
 //          into LDS, then the W_UV projection of the merged rows. With fewer
@@ -114,16 +115,21 @@ __device__ inline void split8(const float* x, typename Mma<WT>::vec& hi, typenam
 // ---------------------------------------------------------------------------
 constexpr int kAbsCols = 128;            // columns per block
 constexpr int kAbsRowBytes = 256 + 32;   // 128 x 16-bit + pad: 4 tr rows hit 4 bank groups
+// Threads per block: 8 waves share the loads (6-8 per wave instead of 14
+// with 4 waves; a wave stalls its issue once about a dozen loads are in
+// flight), 4 of them run the MFMAs. Config 3: 6.6 us per dispatch against
+// 6.8 with 4 waves.
+constexpr int kAbsThreads = 512;
 
 // out_mode 0: q_abs (fp32, (T*nh, dc)). out_mode 1 / 2: q_prep rows (bf16 /
 // fp16, (T*nh, dc + dR)) = [q_abs | q_rope] * scale for the MFMA attention
 // kernel; blocks with cb == 0 also convert the q_rope part of their rows.
 // All global loads (q_nope for every k-step, the W_UK tile) are issued before
-// the first wait.
+// the first wait, spread over the block's 8 waves.
 // NKS = dn / 16 when known at compile time (8 for dn = 128: no guards, every
 // load unconditional), 0 for any dn <= 128 that is a multiple of 16.
 template <typename WT, int NKS>
-__global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restrict__ q_nope, const WT* __restrict__ W,
+__global__ __launch_bounds__(kAbsThreads) void absorb_mfma_kernel(const float* __restrict__ q_nope, const WT* __restrict__ W,
                                                           void* __restrict__ out, int out_mode,
                                                           const float* __restrict__ q_rope, float scale, int dR,
                                                           int tokens, int nh, int dn, int dc, int qps,
@@ -152,7 +158,7 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
   // zero_out: the decode output, which a latent-half merge adds into (every
   // block, before its early return, zeroes a grid-stride share)
   if (zero_out)
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < zero_n; i += (int64_t)gridDim.x * 256)
+    for (int64_t i = (int64_t)blockIdx.x * kAbsThreads + threadIdx.x; i < zero_n; i += (int64_t)gridDim.x * kAbsThreads)
       zero_out[i] = 0.f;
   if (t0 >= tokens || h >= nh) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -160,68 +166,66 @@ __global__ __launch_bounds__(256) void absorb_mfma_kernel(const float* __restric
   if (NKS > 0) dn = 16 * NKS;
 
   // q_nope of token t0 + lane%32, elements 16ks + 8(lane/32) .. +8: wave w
-  // loads k-steps 2w and 2w+1, splits them into hi/lo 16-bit operands and
-  // stages them in LDS for all waves (each wave issues 4 q loads, not 16)
+  // loads k-step w, splits it into hi/lo 16-bit operands and stages them in
+  // LDS for the MFMA waves (each wave issues 2 q loads, not 16)
   const int t = t0 + (lane & 31);
   const bool tvalid = t < tokens;
   const float* qrow = q_nope + ((int64_t)(tvalid ? t : 0) * nh + h) * dn + 8 * (lane >> 5);
-  // (with NKS > 0 every wave's two k-steps exist: the loads go out
+  // (with NKS > 0 every wave's k-step exists: the loads go out
   // unconditionally, since a load under a branch gets its result copied at
   // the branch's end, which waits for it before the W_UK loads below issue)
-  f32x4 qa[2], qb[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int ks = 2 * wave + j;
-    if (NKS > 0 || ks < nks) {
-      qa[j] = *reinterpret_cast<const f32x4*>(qrow + 16 * ks);
-      qb[j] = *reinterpret_cast<const f32x4*>(qrow + 16 * ks + 4);
-    }
+  static_assert(kAbsThreads / 64 == 8, "one q k-step per wave");
+  const int ks_w = wave;
+  f32x4 qa, qb;
+  if (NKS > 0 || ks_w < nks) {
+    qa = *reinterpret_cast<const f32x4*>(qrow + 16 * ks_w);
+    qb = *reinterpret_cast<const f32x4*>(qrow + 16 * ks_w + 4);
   }
   // W_UK[h*dn + i][cb*128 + 0..127] for i < dn, 16 B per thread-load
-  i16x8 wv[8];
+  constexpr int kWLoads = 128 * 16 / kAbsThreads;
+  i16x8 wv[kWLoads];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int q = tid + 256 * k;
-    if (NKS > 0 ? k < NKS : q < dn * 16)
+  for (int k = 0; k < kWLoads; ++k) {
+    const int q = tid + kAbsThreads * k;
+    if (NKS > 0 || q < dn * 16)
       wv[k] = *reinterpret_cast<const i16x8*>(W + ((int64_t)h * dn + (q >> 4)) * dc + cb * kAbsCols + (q & 15) * 8);
   }
   // q_rope rows of the block's tokens for the q_prep rows' rope part, written
   // by the column block 0 of each head: 32 tokens x 64 = one 32-B piece per
-  // thread (dc + dR = 576 on this path, so dR = 64). Loaded here with the
-  // operands, so the tail after the MFMAs is one store, not a load round
-  // trip; by every block (the other column blocks of the head read the same
-  // lines from the XCD's L2) and unconditionally (without q_rope, out_mode 0,
-  // from q_nope instead, unused), since a load under a branch gets its result
-  // copied at the branch's end, which would wait for every load before it.
-  const int rtr = min(t0 + (tid >> 3), tokens - 1);
-  const float* rsrc = out_mode != 0 ? q_rope + ((int64_t)rtr * nh + h) * dR + 8 * (tid & 7) : q_nope;
+  // MFMA-wave thread (dc + dR = 576 on this path, so dR = 64). Loaded here
+  // with the operands, so the tail after the MFMAs is one store, not a load
+  // round trip; by every block (the other column blocks of the head read the
+  // same lines from the XCD's L2) and unconditionally (without q_rope,
+  // out_mode 0, from q_nope instead, unused; waves 4..7 repeat waves 0..3's
+  // pieces), since a load under a branch gets its result copied at the
+  // branch's end, which would wait for every load before it.
+  const int rt = tid & 255;
+  const int rtr = min(t0 + (rt >> 3), tokens - 1);
+  const float* rsrc = out_mode != 0 ? q_rope + ((int64_t)rtr * nh + h) * dR + 8 * (rt & 7) : q_nope;
   const f32x4 ra = *reinterpret_cast<const f32x4*>(rsrc);
   const f32x4 rb = *reinterpret_cast<const f32x4*>(rsrc + 4);
   LA_RSTAMP(1);
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int q = tid + 256 * k;
-    if (NKS > 0 ? k < NKS : q < dn * 16) *reinterpret_cast<i16x8*>(wt + (q >> 4) * kAbsRowBytes + (q & 15) * 16) = wv[k];
+  for (int k = 0; k < kWLoads; ++k) {
+    const int q = tid + kAbsThreads * k;
+    if (NKS > 0 || q < dn * 16) *reinterpret_cast<i16x8*>(wt + (q >> 4) * kAbsRowBytes + (q & 15) * 16) = wv[k];
   }
+  if (NKS > 0 || ks_w < nks) {
+    float x[8];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int ks = 2 * wave + j;
-    if (NKS > 0 || ks < nks) {
-      float x[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        x[e] = tvalid ? qa[j][e] : 0.f;
-        x[4 + e] = tvalid ? qb[j][e] : 0.f;
-      }
-      vec hi, lo;
-      split8<WT>(x, hi, lo);
-      *reinterpret_cast<vec*>(qs + (2 * ks) * 1024 + 16 * lane) = hi;
-      *reinterpret_cast<vec*>(qs + (2 * ks + 1) * 1024 + 16 * lane) = lo;
+    for (int e = 0; e < 4; ++e) {
+      x[e] = tvalid ? qa[e] : 0.f;
+      x[4 + e] = tvalid ? qb[e] : 0.f;
     }
+    vec hi, lo;
+    split8<WT>(x, hi, lo);
+    *reinterpret_cast<vec*>(qs + (2 * ks_w) * 1024 + 16 * lane) = hi;
+    *reinterpret_cast<vec*>(qs + (2 * ks_w + 1) * 1024 + 16 * lane) = lo;
   }
   LA_RSTAMP(2);
   __syncthreads();
   LA_RSTAMP(3);
+  if (wave >= 4) return;  // the loading-only waves are done (no barrier follows)
 
   f32x16 acc_hi = {}, acc_lo = {};
   const int g = lane >> 4, s = lane & 15;
@@ -765,11 +769,11 @@ hipError_t launch_absorb_mfma(const float* q_nope, const void* W_UK, int w_dtype
   const bool d128 = dn == 128;
   if (w_dtype == LA_DTYPE_BF16) {
     auto k = d128 ? absorb_mfma_kernel<__hip_bfloat16, 8> : absorb_mfma_kernel<__hip_bfloat16, 0>;
-    hipLaunchKernelGGL(k, grid, dim3(256), 0, stream, q_nope, reinterpret_cast<const __hip_bfloat16*>(W_UK), out,
+    hipLaunchKernelGGL(k, grid, dim3(kAbsThreads), 0, stream, q_nope, reinterpret_cast<const __hip_bfloat16*>(W_UK), out,
                        out_mode, q_rope, scale, dR, tokens, nh, dn, dc, qps, zero_out, zero_n);
   } else {
     auto k = d128 ? absorb_mfma_kernel<__half, 8> : absorb_mfma_kernel<__half, 0>;
-    hipLaunchKernelGGL(k, grid, dim3(256), 0, stream, q_nope, reinterpret_cast<const __half*>(W_UK), out, out_mode,
+    hipLaunchKernelGGL(k, grid, dim3(kAbsThreads), 0, stream, q_nope, reinterpret_cast<const __half*>(W_UK), out, out_mode,
                        q_rope, scale, dR, tokens, nh, dn, dc, qps, zero_out, zero_n);
   }
   return hipGetLastError();
