@@ -233,6 +233,24 @@ struct Ops<__hip_bfloat16> {
   static __device__ inline void mma_v(f32x16& d, vec a, vec b) {
     asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
   }
+  // mma_v with the A operand's LDS wait (lgkmcnt(N)) in the same asm
+  // statement: as separate statements the compiler pads a wait state between
+  // them. mma_v_lvw / mma_v0_lvw: also the wait for the Q loads of operands b
+  // and q1 .. q5 (vmcnt(M)), which the statement marks as produced.
+  template <int N>
+  static __device__ inline void mma_v_lw(f32x16& d, vec a, vec b) {
+    asm volatile("s_waitcnt lgkmcnt(%3)\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b), "n"(N));
+  }
+  template <int N, int M>
+  static __device__ inline void mma_v_lvw(f32x16& d, vec a, vec b, vec& q1, vec& q2, vec& q3, vec& q4, vec& q5) {
+    asm volatile("s_waitcnt vmcnt(%9) lgkmcnt(%8)\n\tv_mfma_f32_32x32x16_bf16 %0, %6, %7, %0"
+                 : "+v"(d), "+v"(q1), "+v"(q2), "+v"(q3), "+v"(q4), "+v"(q5) : "v"(a), "v"(b), "n"(N), "n"(M));
+  }
+  template <int N, int M>
+  static __device__ inline void mma_v0_lvw(f32x16& d, vec a, vec b, vec& q1, vec& q2, vec& q3, vec& q4, vec& q5) {
+    asm volatile("s_waitcnt vmcnt(%9) lgkmcnt(%8)\n\tv_mfma_f32_32x32x16_bf16 %0, %6, %7, 0"
+                 : "=&v"(d), "+v"(q1), "+v"(q2), "+v"(q3), "+v"(q4), "+v"(q5) : "v"(a), "v"(b), "n"(N), "n"(M));
+  }
   static __device__ inline void mma_a(f32x16& d, vec a, vec b) {
     asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
   }
@@ -253,6 +271,24 @@ struct Ops<__half> {
   }
   static __device__ inline void mma_v(f32x16& d, vec a, vec b) {
     asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+  }
+  // mma_v with the A operand's LDS wait (lgkmcnt(N)) in the same asm
+  // statement: as separate statements the compiler pads a wait state between
+  // them. mma_v_lvw / mma_v0_lvw: also the wait for the Q loads of operands b
+  // and q1 .. q5 (vmcnt(M)), which the statement marks as produced.
+  template <int N>
+  static __device__ inline void mma_v_lw(f32x16& d, vec a, vec b) {
+    asm volatile("s_waitcnt lgkmcnt(%3)\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b), "n"(N));
+  }
+  template <int N, int M>
+  static __device__ inline void mma_v_lvw(f32x16& d, vec a, vec b, vec& q1, vec& q2, vec& q3, vec& q4, vec& q5) {
+    asm volatile("s_waitcnt vmcnt(%9) lgkmcnt(%8)\n\tv_mfma_f32_32x32x16_f16 %0, %6, %7, %0"
+                 : "+v"(d), "+v"(q1), "+v"(q2), "+v"(q3), "+v"(q4), "+v"(q5) : "v"(a), "v"(b), "n"(N), "n"(M));
+  }
+  template <int N, int M>
+  static __device__ inline void mma_v0_lvw(f32x16& d, vec a, vec b, vec& q1, vec& q2, vec& q3, vec& q4, vec& q5) {
+    asm volatile("s_waitcnt vmcnt(%9) lgkmcnt(%8)\n\tv_mfma_f32_32x32x16_f16 %0, %6, %7, 0"
+                 : "=&v"(d), "+v"(q1), "+v"(q2), "+v"(q3), "+v"(q4), "+v"(q5) : "v"(a), "v"(b), "n"(N), "n"(M));
   }
   static __device__ inline void mma_a(f32x16& d, vec a, vec b) {
     asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
@@ -319,22 +355,15 @@ __device__ inline void wait_vm_ext() {
 // the tile copies of QK steps before kk (copy m at step copy_step(m), m <
 // copies) and, paged, the table entry load before the phase. In every later
 // QK phase only those copies and that entry are outstanding, so the same
-// wait never binds there.
+// wait never binds there. The wait goes into the MFMA's asm statement
+// (mma_v_lvw), which also marks q[KK+1 .. KK+5] as produced there.
 template <int KK, int Copies, bool Paged>
 constexpr int qb_vm_n() {
+  static_assert(KK % 6 == 0 && KK + 5 < 36, "six k-steps per wait");
   int c = 0;
   for (int m = 0; m < Copies; ++m)
     if (copy_step(m) < KK) ++c;
   return (30 - KK) + c + (Paged ? 1 : 0);
-}
-template <int KK, int Copies, bool Paged, typename V>
-__device__ inline void qb_wait(V (&q)[36]) {
-  static_assert(KK % 6 == 0 && KK + 5 < 36, "six k-steps per wait");
-  constexpr int N = qb_vm_n<KK, Copies, Paged>();
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%6)"
-               : "+v"(q[KK]), "+v"(q[KK + 1]), "+v"(q[KK + 2]), "+v"(q[KK + 3]), "+v"(q[KK + 4]), "+v"(q[KK + 5])
-               : "n"(N));
 }
 
 // LDS-visibility barrier that leaves outstanding HBM->LDS copies in flight.
@@ -989,7 +1018,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     // when that row's head does).
     // The 36 loads are inline asm, after tile 0's copies: the compiler does
     // not track them, and the first QK phase waits for them k-step group by
-    // k-step group (qb_wait), so it overlaps the loads' tail.
+    // k-step group (qb_vm_n), so it overlaps the loads' tail.
     vec qb[36];
     {
       const int q_lane = lane_id();
@@ -1161,13 +1190,17 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           pp[1] = lds_rd128<vec>(L, pp_x + 1024);
         }
         vec& a = ar[kk % D];
-        wait_lgkm<qk_later(kk)>(a);
-        if constexpr (kk % 6 == 0) qb_wait<kk, kDma, kPaged>(qb);
-        if constexpr (kk < 32) {
-          if constexpr (kk == 0) O_::mma_v0(s_next, a, qb[kk]);
-          else O_::mma_v(s_next, a, qb[kk]);
+        // the operand's wait (and every sixth step the wait for Q k-steps kk
+        // .. kk+5, qb_vm_n) in the MFMA's asm statement
+        if constexpr (kk % 6 == 0) {
+          constexpr int M = qb_vm_n<kk, kDma, kPaged>();
+          static_assert(M >= 0 && M < 64, "vmcnt range");
+          if constexpr (kk == 0)
+            O_::template mma_v0_lvw<qk_later(kk), M>(s_next, a, qb[kk], qb[kk + 1], qb[kk + 2], qb[kk + 3], qb[kk + 4], qb[kk + 5]);
+          else
+            O_::template mma_v_lvw<qk_later(kk), M>(s_next, a, qb[kk], qb[kk + 1], qb[kk + 2], qb[kk + 3], qb[kk + 4], qb[kk + 5]);
         } else {
-          O_::mma_v(s_next, a, qb[kk]);
+          O_::template mma_v_lw<qk_later(kk)>(s_next, a, qb[kk]);
         }
         if constexpr (kk + D < 36) a = a_rd(std::integral_constant<int, kk + D>());
         constexpr int cm = (kk - kCopyFirst) / kCopyStride;  // the copy of this step, if any
