@@ -140,6 +140,10 @@ constexpr int kQrAt = 32 - kQkDepth;   // QK step before which the partner-P rea
 constexpr int kTrAt = 36 - kPvDepth;   // QK steps kTrAt.. issue the first kPvDepth PV value-read pairs
 constexpr int kSmSettle = 1;           // softmax slot (two per PV step) that starts softmax(t+1)
 constexpr int kSmExp0 = 8;             // softmax slots kSmExp0 .. +17: the 3-stage exp2 pipeline
+// the softmax's slots in order: settle / mask, 4 max-tree slots, the running
+// max (kSmSettle + 5), then the exp2 pipeline: overlapping ranges would drop
+// a piece (each slot runs one branch of sm_piece)
+static_assert(kSmExp0 > kSmSettle + 5 && kSmExp0 + 18 < 2 * kPvSteps, "softmax slots in order, inside PV");
 
 // LDS issue order of one iteration (all reads counted by lgkmcnt):
 //   QK:  [partner flag] A(0..D-1); per step kk: [kk == kQrAt: 2 partner-P
