@@ -61,10 +61,15 @@ namespace la {
 //   4 tile 0 landed  5 tile 0 rotated  6 loop at t = 0 (after iteration -1)
 //   7 loop done  8 past the staging barrier  9 partial stores issued
 //   10 stores complete
+// and, summed over the iterations t >= 0 of the segment, the cycles of each
+// iteration's parts: 11 the barrier (from the iteration's start), 12 QK(t+1)
+// with the copies of tile t+2, 13 PV(t) with softmax(t+1), the RoPE of tile
+// t+2 and the P publication, 14 the wait for the iteration's copies; 15 the
+// number of those iterations.
 // A stamp waits for the scalar data path (lgkmcnt), which drains the wave's
 // LDS queue: the instrumented kernel runs a few per cent slower.
 #ifdef LA_PHASE_STAMPS
-constexpr int kStampSlots = 12;
+constexpr int kStampSlots = 16;
 constexpr int kStampBlocks = 4096;
 __device__ unsigned long long g_attn_stamps[kStampBlocks * 4 * kStampSlots];
 #define LA_STAMP(i)                                                                                  \
@@ -73,6 +78,7 @@ __device__ unsigned long long g_attn_stamps[kStampBlocks * 4 * kStampSlots];
     asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t_)::"memory");                       \
     stamps_[i] = t_;                                                                                 \
   } while (0)
+#define LA_TSTAMP(v) asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v)::"memory")
 #else
 #define LA_STAMP(i) ((void)0)
 #endif
@@ -989,6 +995,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     const int ntiles = (seg_len + kT - 1) / kT;
 
     LA_STAMP(1);
+#ifdef LA_PHASE_STAMPS
+    for (int i = 11; i < 16; ++i) stamps_[i] = 0;
+#endif
     lds_barrier();  // all waves are done with the previous segment's buffers
     LA_STAMP(2);
 
@@ -1105,10 +1114,17 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
 #ifdef LA_PHASE_STAMPS
       if (t == 0) LA_STAMP(6);
 #endif
+#ifdef LA_PHASE_STAMPS
+      unsigned long long tt0, tt1, tt2, tt3, tt4;
+      LA_TSTAMP(tt0);
+#endif
       // this wave's copies of tile t+1 were waited for at the end of
       // iteration t-1 (t = -1: tile 0 in the prologue; the Q loads are still
       // in flight and QK(0) waits for them group by group)
       lds_barrier();  // tile t+1 staged and rotated by every wave; iteration t-1 done
+#ifdef LA_PHASE_STAMPS
+      LA_TSTAMP(tt1);
+#endif
       const int lane = lane_id();
       const int g2 = lane >> 5;
       const int q16 = lane >> 4, s16 = lane & 15;
@@ -1226,6 +1242,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         s_next = f32x16{};
       }
 
+#ifdef LA_PHASE_STAMPS
+      LA_TSTAMP(tt2);
+#endif
       // ---- softmax(t+1) pieces, spread over the PV(t) steps ----
       // s_next lane = head, 16 positions 8(i/4) + 4*g2 + (i%4); lazy base-2
       // online softmax: P = 2^(s - m) with m raised only when a score exceeds
@@ -1435,8 +1454,21 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         if (lane < 32) lds_st(L, natab + 4 * lane, alpha_pend);
         if (lane == 0) lds_st(L, natab + 128, resc_pend ? 1.f : 0.f);
       }
+#ifdef LA_PHASE_STAMPS
+      LA_TSTAMP(tt3);
+#endif
       wait_vm<0>();  // this wave's copies of tile t+2 (issued in this iteration) have landed
       if constexpr (kPaged) tie(blk_cur);  // and the table entry loaded with them
+#ifdef LA_PHASE_STAMPS
+      LA_TSTAMP(tt4);
+      if (t >= 0) {
+        stamps_[11] += tt1 - tt0;
+        stamps_[12] += tt2 - tt1;
+        stamps_[13] += tt3 - tt2;
+        stamps_[14] += tt4 - tt3;
+        stamps_[15] += 1;
+      }
+#endif
     }
 
     LA_STAMP(7);
@@ -1571,7 +1603,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   LA_STAMP(10);
   if ((threadIdx.x & 63) == 0 && blockIdx.x < kStampBlocks)
-    for (int i = 0; i < 11; ++i) g_attn_stamps[((size_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kStampSlots + i] = stamps_[i];
+    for (int i = 0; i < kStampSlots; ++i) g_attn_stamps[((size_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kStampSlots + i] = stamps_[i];
 #endif
 }
 

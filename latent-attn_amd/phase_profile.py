@@ -9,7 +9,10 @@ prints, per workload:
 * the attention kernel (``decode_mfma_kernel``): shader-clock cycles per wave
   of each phase, mean and max over the waves of all workgroups, for two
   launches: the 10th of 10 identical launches back to back, and the launch
-  inside a normal step (after the absorb kernel);
+  inside a normal step (after the absorb kernel); and the mean cycles per
+  tile of each part of a loop iteration (barrier, QK phase, PV phase, wait
+  for the iteration's copies), summed over the iterations and divided by
+  their number;
 * the absorb and merge + projection kernels: wave 0 of each block on the
   device's constant 100 MHz clock (common to all XCDs), so the block start
   spread and every phase are in microseconds on one time line.
@@ -51,6 +54,12 @@ ATTN_PHASES = [
     "staging + partial stores issued",
     "stores complete",
 ]
+TILE_PARTS = [
+    "barrier (from the iteration's start)",
+    "QK(t+1): 36 score MFMAs, 11 copies of tile t+2, partner P and first value reads",
+    "PV(t): 32 value MFMAs, softmax(t+1), RoPE of tile t+2, P publication",
+    "wait for the iteration's copies",
+]
 ABSORB_PHASES = ["issue loads", "wait data, LDS stores", "barrier", "MFMAs", "stores complete"]
 MERGE_PHASES = ["issue W_UV loads", "merge (wave 0)", "other waves + LDS sums", "projection MFMAs", "stores complete"]
 
@@ -72,16 +81,22 @@ def load_phase_lib():
     return capi, lib
 
 
+SLOTS = 16  # kStampSlots in la_mfma.hip
+
+
 def attn_table(lib, blocks: int):
     import numpy as np
 
-    buf = (ctypes.c_ulonglong * (48 * blocks))()
+    buf = (ctypes.c_ulonglong * (4 * SLOTS * blocks))()
     assert lib.la_phase_attn_stamps(buf, blocks, 0) == 0
-    a = np.frombuffer(buf, dtype=np.uint64).reshape(blocks, 4, 12).astype(np.int64)
-    a = a[a[:, 0, 10] > 0][:, :, :11]  # workgroups that ran to the end
+    full = np.frombuffer(buf, dtype=np.uint64).reshape(blocks, 4, SLOTS).astype(np.int64)
+    full = full[full[:, 0, 10] > 0]  # workgroups that ran to the end
+    a = full[:, :, :11]
     d = np.diff(a, axis=2)
     total = a[:, :, 10] - a[:, :, 0]
-    return len(a), total, d
+    n = np.maximum(full[:, :, 15], 1)
+    per_tile = full[:, :, 11:15] / n[:, :, None]  # (workgroups, waves, 4 parts)
+    return len(a), total, d, per_tile
 
 
 def side_table(lib, kind: int, blocks: int):
@@ -157,6 +172,12 @@ def main() -> None:
             print(f"| {ph} | {b.mean():.0f} | {b.max():.0f} | {s.mean():.0f} | {s.max():.0f} |")
         tb, ts = rows["back to back"][1], rows["in a step"][1]
         print(f"| total | {tb.mean():.0f} | {tb.max():.0f} | {ts.mean():.0f} | {ts.max():.0f} |")
+        print("\n| loop iteration part (cycles per tile, mean over waves) | back to back | in a step |")
+        print("|---|---|---|")
+        pb, ps = rows["back to back"][3], rows["in a step"][3]
+        for i, part in enumerate(TILE_PARTS):
+            print(f"| {part} | {pb[:, :, i].mean():.0f} | {ps[:, :, i].mean():.0f} |")
+        print(f"| iteration | {pb.sum(axis=2).mean():.0f} | {ps.sum(axis=2).mean():.0f} |")
         # absorb and merge of that step
         for kind, kname, phases in ((0, "absorb", ABSORB_PHASES), (1, "merge + projection", MERGE_PHASES)):
             a = side_table(lib, kind, 8192)
