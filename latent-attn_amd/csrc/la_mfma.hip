@@ -1110,6 +1110,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       ltb0 = tc + ct_row_off(4 * (q16 >> 1) + (s16 >> 2));
       ltb1 = tc + ct_row_off(8 + 4 * (q16 >> 1) + (s16 >> 2));
     }
+    // buffers of tiles t, t+1, t+2 (iteration -1: tile 0 in both of the
+    // first two), carried from iteration to iteration
+    uint32_t cur_b = 0, nxt_b = 0, dbuf_b = kBufBytes;
     for (int t = -1; t < ntiles; ++t) {
 #ifdef LA_PHASE_STAMPS
       if (t == 0) LA_STAMP(6);
@@ -1130,9 +1133,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       const int q16 = lane >> 4, s16 = lane & 15;
       const int head = 32 * wave + (lane & 31);
       const bool sm = t + 1 < ntiles;  // softmax(t+1) runs in this iteration
-      const uint32_t cur = ((t < 0 ? 0 : t) % kNBuf) * kBufBytes;  // t = -1: tile 0, with P = 0
-      const uint32_t nxt = ((t + 1) % kNBuf) * kBufBytes;
-      const uint32_t dbuf = ((t + 2) % kNBuf) * kBufBytes;
+      const uint32_t cur = cur_b, nxt = nxt_b, dbuf = dbuf_b;
       const int par = t & 1;  // tables of P(t) and of softmax(t)'s rescale
       const uint32_t atab = kAtabOff + par * kAtabPar;
 
@@ -1166,13 +1167,13 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // the phase (no tile t+1).
       const int arow = lane & 31;
       const uint32_t ct_x = nxt + lct;
-      const uint32_t rp_x = nxt + kRopeOff + lrp;  // nxt + kRopeOff is a multiple of 128
-      const uint32_t pp_x = kPtabOff + par * kPtabPar + pw * 2048 + 16 * lane;
+      uint32_t rp_x, pp_x;
       // paged: this iteration's copies use tile t+2's entry (loaded in the
       // previous iteration or the prologue); tile t+3's goes out now and is
       // waited for by the next iteration's vmcnt(0)
-      const TileDma dm = tile_dma<kFp8>(sg, t + 2, tile_base<kPaged, kFp8>(p, sg, t + 2, blk_cur), wave, lane);
+      const int ent2 = kPaged ? __builtin_amdgcn_readfirstlane(blk_cur) : 0;
       if constexpr (kPaged) tile_block_entry_async(p, sg, t + 3, blk_cur);
+      TileDma dm;
       auto a_rd = [&](auto kk_c) -> vec {
         constexpr int kk = decltype(kk_c)::value;
         if constexpr (kk < 32) return lds_rd128<vec, 32 * kk>(L, ct_x);
@@ -1186,8 +1187,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       // ct_row_off(rho) = 16ks kRowPitch + ct_row_off(rho - 16ks), so read x
       // is lane base tb_x plus the immediate 16ks kRowPitch + 64nb; this
       // wave's column blocks are nb = 8ch + cb.
-      const uint32_t tb0 = cur + ltb0;
-      const uint32_t tb1 = cur + ltb1;
+      uint32_t tb0, tb1;
       TrPair tr[kPvDepth];
       auto b_issue = [&](TrPair& r, auto step_c) {
         constexpr int step = decltype(step_c)::value;
@@ -1195,6 +1195,35 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         r.x0 = lds_tr<16 * kRowPitch * ks + 64 * cb>(L, tb0);
         r.x1 = lds_tr<16 * kRowPitch * ks + 64 * cb>(L, tb1);
       };
+
+      // Addresses the QK phase needs only later are made inside it, in the
+      // issue slack between its MFMAs (the empty asm statements keep each
+      // computation at its step), not between the barrier and the first
+      // MFMA: the copies' addresses of tile t+2 after step 0, the partner-P
+      // address after step 20, the k_rope operand address after step 22, the
+      // value-read bases after step 28.
+      auto qk_setup = [&](auto kk_c) {
+        constexpr int kk = decltype(kk_c)::value;
+        if constexpr (kk == 0) {
+          int t2 = t + 2;
+          asm volatile("" : "+s"(t2));
+          dm = tile_dma<kFp8>(sg, t2, tile_base<kPaged, kFp8>(p, sg, t2, ent2), wave, lane);
+        } else if constexpr (kk == 20) {
+          uint32_t pb = kPtabOff + par * kPtabPar + pw * 2048;
+          asm volatile("" : "+s"(pb));
+          pp_x = pb + 16 * lane;
+        } else if constexpr (kk == 22) {
+          uint32_t nb = nxt;
+          asm volatile("" : "+s"(nb));
+          rp_x = nb + kRopeOff + lrp;  // nxt + kRopeOff is a multiple of 128
+        } else if constexpr (kk == 28) {
+          uint32_t cb = cur;
+          asm volatile("" : "+s"(cb));
+          tb0 = cb + ltb0;
+          tb1 = cb + ltb1;
+        }
+      };
+      static_assert(kQrAt > 20 && 32 - kQkDepth > 22 && kTrAt > 28, "setup before first use");
 
       f32x16 s_next;
       vec pp[2];  // partner's P(t), read at step kQrAt
@@ -1229,6 +1258,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           else issue_copy<dma_order(cm)>(p, sg, t + 2, L, dbuf, wave, lane, dm);
         }
         if constexpr (kk >= kTrAt && kk - kTrAt < kPvDepth) b_issue(tr[kk - kTrAt], std::integral_constant<int, kk - kTrAt>());
+        qk_setup(kk_c);
         __builtin_amdgcn_sched_barrier(0);
       });
       } else {
@@ -1236,6 +1266,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         // that PV(t) waits for go out, in QK's order (partner P, then the
         // first kPvDepth value-read pairs), so PV's static counts still hold.
         pflag = lds_rd32_now(pflag_at);
+        pp_x = kPtabOff + par * kPtabPar + pw * 2048 + 16 * lane;
+        tb0 = cur + ltb0;
+        tb1 = cur + ltb1;
         pp[0] = lds_rd128<vec>(L, pp_x);
         pp[1] = lds_rd128<vec>(L, pp_x + 1024);
         static_for<kPvDepth>([&](auto i) { b_issue(tr[decltype(i)::value], i); });
@@ -1469,6 +1502,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         stamps_[15] += 1;
       }
 #endif
+      cur_b = nxt_b;
+      nxt_b = dbuf_b;
+      dbuf_b = kNBuf * kBufBytes - cur_b - nxt_b;
     }
 
     LA_STAMP(7);
