@@ -316,7 +316,11 @@ __device__ inline void settle(f32x16& d0, f32x16& d1) {
   asm volatile("s_nop 15\n\ts_nop 15" : "+v"(d0), "+v"(d1));
 }
 
-__device__ inline void settle1(f32x16& d0) { asm volatile("s_nop 15\n\ts_nop 15" : "+v"(d0)); }
+// The QK accumulator before softmax(t+1) reads it (PV slot kSmSettle = 1):
+// 16 wait states, and the code between the last QK MFMA and that slot issues
+// at least 7 more instructions (step 35's two value reads, PV step 0's wait,
+// its two MFMAs and step 4's two value reads), 23 in all.
+__device__ inline void settle1(f32x16& d0) { asm volatile("s_nop 15" : "+v"(d0)); }
 
 // 32 wait states before the O accumulators (AGPRs written by MFMAs) are read
 // or rewritten by VALU code; every later access is ordered after it.
@@ -606,6 +610,11 @@ struct SegCtx {
   int seq;           // sequence
   const int32_t* tab;  // paged cache: the sequence's block-table row
   uint32_t tile0;      // paged cache: in-sequence tile index of the segment's first tile
+  // RoPE table row of position pos0 + r, r >= 0: min(pc + r, rlim), where
+  // rlim = rope_rows - 1 (INT32_MAX when unchecked) and pc = min(pos0, rlim):
+  // the clamp of rope_row in 32 bits (the MFMA kernels' positions and table
+  // rows stay below 2^24 + 2^20, mfma_supported)
+  int pc, rlim;
 };
 
 // Tile k covers segment rows [32k, 32k + 32). The pipeline also copies up to
@@ -662,7 +671,16 @@ struct TileDma {
   uint32_t ct, rope;
   int dlast;  // last - tb, wave-uniform
 };
+// The k_rope copy's offset alone (rope of tile_dma): row delta below 64, so
+// a 24-bit multiply.
 template <bool kFp8>
+__device__ inline uint32_t tile_dma_rope(const SegCtx& sg, int k, int wave, int lane) {
+  if constexpr (kFp8) return 0u;
+  const int tb = k * kT + 8 * wave, t0 = tile_eff(sg, k) * kT, rr = lane >> 3;
+  return __umul24((uint32_t)(min(tb + rr, sg.last) - t0), (uint32_t)cache_row_bytes<kFp8>()) + kDc * 2 +
+         16 * ((lane & 7) ^ fr(8 * wave + rr));
+}
+template <bool kFp8, bool kRope = true>
 __device__ inline TileDma tile_dma(const SegCtx& sg, int k, const char* base, int wave, int lane) {
   constexpr int kRowB = cache_row_bytes<kFp8>();
   const int tb = k * kT + 8 * wave;
@@ -672,7 +690,8 @@ __device__ inline TileDma tile_dma(const SegCtx& sg, int k, const char* base, in
   d.base = base;
   d.ct = (uint32_t)(tb - t0) * kRowB + 16 * lane;
   d.dlast = sg.last - tb;
-  d.rope = kFp8 ? 0u : (uint32_t)(min(tb + rr, sg.last) - t0) * kRowB + kDc * 2 + 16 * ((lane & 7) ^ fr(8 * wave + rr));
+  (void)rr;
+  d.rope = kRope ? tile_dma_rope<kFp8>(sg, k, wave, lane) : 0u;
   return d;
 }
 
@@ -696,7 +715,7 @@ __device__ inline void issue_copy(const DecodeProblem& p, const SegCtx& sg, int 
   } else {
     const int row = r_first + (lane >> 3);
     const int r = min(k * kT + row, sg.last);
-    const uint32_t toff = (uint32_t)(rope_row(p, sg.pos0 + r) * (kDr / 2) * 4 + (lane & 7) * 16);
+    const uint32_t toff = (uint32_t)min(sg.pc + r, sg.rlim) * ((kDr / 2) * 4) + (lane & 7) * 16;
     const float* tab = J == 9 ? p.rope_cos : p.rope_sin;
     __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(tab) + toff,
                                      (lds_void*)(L + (J == 9 ? kCosOff : kSinOff) + r_first * 128), 16, 0, 0);
@@ -780,6 +799,22 @@ __device__ inline RotIn rot_issue(const lchar* L, uint32_t buf, int wave, int la
   }
   r.c = lds_rd128<f32x4>(L, kCosOff + row * 128 + 16 * u);
   r.s = lds_rd128<f32x4>(L, kSinOff + row * 128 + 16 * u);
+  return r;
+}
+
+// rot_issue for a 16-bit cache from precomputed addresses: pa = buf +
+// kRopeOff + the lane part (row 8w + lane/8, chunk (lane%8)/2 ^ fr(row),
+// half lane%2); the chunk of elements i + 32 is that of i XOR 4, so pb = pa ^
+// 64 (rows are 128-aligned); cs = kCosOff + 1024w + 16 lane, the sin row at
+// the same offset from kSinOff.
+__device__ inline RotIn rot_issue_at(const lchar* L, uint32_t pa, uint32_t cs) {
+  RotIn r;
+  r.pa = pa;
+  r.pb = pa ^ 64;
+  r.ka = lds_rd64(L, r.pa);
+  r.kb = lds_rd64(L, r.pb);
+  r.c = lds_rd128<f32x4>(L, cs);
+  r.s = lds_rd128<f32x4, kSinOff - kCosOff>(L, cs);
   return r;
 }
 
@@ -991,6 +1026,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     sg.seq = s;
     sg.tab = kPaged ? p.block_table + (int64_t)s * p.blocks_per_seq : nullptr;
     sg.tile0 = (uint32_t)(sg.pos0 / kT);
+    sg.rlim = p.rope_rows > 0 ? (int)(p.rope_rows - 1) : INT32_MAX;
+    sg.pc = (int)min(sg.pos0, (int64_t)sg.rlim);
     const int seg_len = sg.last + 1;
     const int ntiles = (seg_len + kT - 1) / kT;
 
@@ -1100,12 +1137,18 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
     }
     // lane parts of the loop's LDS addresses (the buffer offsets are
     // per-iteration scalars added to them)
-    int lct, lrp, ltb0, ltb1;
+    int lct, lrp, ltb0, ltb1, lrot, lr1152, lrope;
     {
       const int ln = lane_id();
       const int ar = ln & 31, gg = ln >> 5, q16 = ln >> 4, s16 = ln & 15;
       lct = ct_row_off(ar) + 16 * gg;
       lrp = ar * 128 + 16 * (gg ^ fr(ar));
+      const int rrow = 8 * wave + (ln >> 3), ru = ln & 7;
+      lrot = rrow * 128 + (((ru >> 1) ^ fr(rrow)) << 4) + 8 * (ru & 1);
+      // the k_rope copy's lane parts (tile_dma_rope): row 8w + lane/8 times
+      // the row bytes, and the swizzled chunk past the latent part
+      lr1152 = rrow * cache_row_bytes<kFp8>();
+      lrope = kDc * 2 + 16 * (ru ^ fr(rrow));
       const int tc = 32 * (q16 & 1) + 8 * (s16 & 3) + 512 * ch;
       ltb0 = tc + ct_row_off(4 * (q16 >> 1) + (s16 >> 2));
       ltb1 = tc + ct_row_off(8 + 4 * (q16 >> 1) + (s16 >> 2));
@@ -1207,7 +1250,16 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         if constexpr (kk == 0) {
           int t2 = t + 2;
           asm volatile("" : "+s"(t2));
-          dm = tile_dma<kFp8>(sg, t2, tile_base<kPaged, kFp8>(p, sg, t2, ent2), wave, lane);
+          dm = tile_dma<kFp8, false>(sg, t2, tile_base<kPaged, kFp8>(p, sg, t2, ent2), wave, lane);
+        } else if constexpr (kk == 1 && !kFp8) {
+          // tile_dma_rope from the lane parts: (min(tb + lane/8, last) - t0)
+          // row bytes = min(lo + lr1152, hi), tb = 32 t2 + 8w, t0 its tile's
+          // first row (tile_eff)
+          int t2 = t + 2;
+          asm volatile("" : "+s"(t2));
+          const int t0 = tile_eff(sg, t2) * kT;
+          const int lo = (t2 * kT - t0) * kRowBytes, hi = (sg.last - t0) * kRowBytes;
+          dm.rope = (uint32_t)(min(lo + lr1152, hi) + lrope);
         } else if constexpr (kk == 20) {
           uint32_t pb = kPtabOff + par * kPtabPar + pw * 2048;
           asm volatile("" : "+s"(pb));
@@ -1223,7 +1275,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           tb1 = cb + ltb1;
         }
       };
-      static_assert(kQrAt > 20 && 32 - kQkDepth > 22 && kTrAt > 28, "setup before first use");
+      static_assert(kQrAt > 20 && 32 - kQkDepth > 22 && kTrAt > 28 && kCopyFirst > 1, "setup before first use");
 
       f32x16 s_next;
       vec pp[2];  // partner's P(t), read at step kQrAt
@@ -1466,7 +1518,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           // fp8 tile's k_rope parts come with every row copy)
           if constexpr (kFp8) wait_vm<0>();
           else wait_vm<kDmaPerWave - 3>();
-          rot = rot_issue<kFp8>(L, dbuf, wave, lane);
+          if constexpr (kFp8) rot = rot_issue<kFp8>(L, dbuf, wave, lane);
+          else rot = rot_issue_at(L, dbuf + kRopeOff + lrot, kCosOff + 1024 * wave + 16 * lane);
           if constexpr (kFp8) fp8_exp_issue<0>(e_src, xe);
         }
         sm_piece(std::integral_constant<int, 2 * step + 1>());
