@@ -12,9 +12,12 @@ the newest N), and any other instruction that reads or writes a register a
 pending read will write is reported (vector-memory loads can be tracked the
 same way against vmcnt).
 
-The walk is linear: branches are not followed, so code of a skipped arm is
-scanned in place. That over-approximates the pending set on some paths and
-is exact on the straight-line hot loop.
+pending_uses walks linearly: branches are not followed, so code of a
+skipped arm is scanned in place, which over-approximates the pending set on
+some paths and is exact on the straight-line hot loop. pending_uses_cfg walks
+the control-flow graph instead (labels kept by kernels_with_labels), so a
+branch arm is checked with the state of the paths that reach it, loops
+included.
 """
 
 from __future__ import annotations
@@ -132,3 +135,125 @@ def pending_uses(instrs: list, counters=("lgkm",)) -> list:
         elif vmem:
             pend["vm"].append((_regs(ops[0]) if is_load else set(), n))
     return bad
+
+
+def kernels_with_labels(asm: str, prefix: str) -> dict:
+    """As kernels(), but branch-target labels stay in the lists as "Lname:"
+    entries (for pending_uses_cfg)."""
+    out, cur = {}, None
+    for line in asm.splitlines():
+        m = re.match(r"^(\S+):", line)
+        if m and m.group(1).startswith(prefix):
+            cur = m.group(1)
+            out[cur] = []
+            continue
+        if cur is None:
+            continue
+        if line.startswith(".Lfunc_end"):
+            cur = None
+            continue
+        s = line.strip()
+        lm = re.match(r"^(\.?L\w*):", s)
+        if lm:
+            out[cur].append(lm.group(1) + ":")
+        elif s and not s.startswith((";", ".")):
+            out[cur].append(s)
+    return out
+
+
+def _blocks(lines: list):
+    """Basic blocks of a labelled instruction list: [(start, end)] over the
+    instruction indices (labels removed), the label -> block map, and each
+    block's successors."""
+    instrs, labels_at = [], {}
+    for ln in lines:
+        if ln.endswith(":") and " " not in ln:
+            labels_at.setdefault(len(instrs), []).append(ln[:-1])
+        else:
+            instrs.append(ln)
+    starts = {0} | set(labels_at)
+    for i, ins in enumerate(instrs):
+        op = ins.split()[0]
+        if op.startswith(("s_branch", "s_cbranch", "s_setpc", "s_endpgm")):
+            starts.add(i + 1)
+    starts = sorted(s for s in starts if s < len(instrs))
+    blocks = [(s, (starts[k + 1] if k + 1 < len(starts) else len(instrs))) for k, s in enumerate(starts)]
+    block_of = {s: k for k, (s, _) in enumerate(blocks)}
+    label_block = {name: block_of[i] for i, names in labels_at.items() if i in block_of for name in names}
+    succ = []
+    for k, (s, e) in enumerate(blocks):
+        last = instrs[e - 1].split()
+        op = last[0]
+        nxt = [k + 1] if k + 1 < len(blocks) else []
+        if op == "s_branch":
+            succ.append([label_block[last[1]]])
+        elif op in ("s_cbranch_execz", "s_cbranch_execnz") and e - 2 >= s and instrs[e - 2].startswith("s_and_saveexec"):
+            # the branch of a divergent if: its all-lanes-inactive outcome is not followed
+            succ.append(nxt if op == "s_cbranch_execz" else [label_block[last[1]]])
+        elif op.startswith("s_cbranch"):
+            succ.append([label_block[last[1]]] + nxt)
+        elif op.startswith(("s_setpc", "s_endpgm")):
+            succ.append([])
+        else:
+            succ.append(nxt)
+    return instrs, blocks, succ
+
+
+def pending_uses_cfg(lines: list, counters=("lgkm",), max_states=256) -> list:
+    """pending_uses along the control-flow graph of a labelled instruction
+    list (kernels_with_labels): every branch edge is followed with the
+    in-order counter state of the path that reaches it (each distinct state
+    once per block; states are compared by their pending destination
+    registers), so the arm a branch skips is not scanned in place. The
+    all-lanes-inactive outcome of a divergent if (an exec branch right after
+    s_and_saveexec: the taken edge of s_cbranch_execz, the fall-through of
+    s_cbranch_execnz) is not followed: the kernels issue every memory
+    operation that a static count includes with some lane active (a
+    lane-subset copy or store always has lanes), which is the invariant those
+    counts rest on. Other exec branches (loops over lanes) keep both edges."""
+    instrs, blocks, succ = _blocks(lines)
+    bad, seen = {}, {}
+    work = [(0, ((), ()))]
+    while work:
+        k, state = work.pop()
+        key = (tuple(d for d, _ in state[0]), tuple(d for d, _ in state[1]))
+        if key in seen.setdefault(k, set()):
+            continue
+        if len(seen[k]) >= max_states:
+            raise RuntimeError("too many counter states at one block")
+        seen[k].add(key)
+        pend = {"lgkm": [(set(d), i) for d, i in state[0]], "vm": [(set(d), i) for d, i in state[1]]}
+        s, e = blocks[k]
+        for n in range(s, e):
+            ins = instrs[n]
+            op = ins.split()[0]
+            if op == "s_waitcnt":
+                for cnt in ("lgkm", "vm"):
+                    m = re.search(cnt + r"cnt\((\d+)\)", ins)
+                    if m:
+                        pend[cnt] = _retire(pend[cnt], int(m.group(1)))
+                continue
+            ops = _operands(ins)
+            is_load = op.startswith(("global_load", "buffer_load")) and "_lds_" not in op
+            vmem = op.startswith(("global_", "buffer_", "scratch_"))
+            reads_dest = op.startswith("ds_read") or is_load
+            used = set()
+            for o in ops[1:] if reads_dest else ops:
+                used |= _regs(o)
+            for cnt in counters:
+                for dest, at in pend[cnt]:
+                    if dest & used and not _dead_high_half_read(instrs, n, dest & used):
+                        bad[(n, at)] = (n, ins, at, instrs[at])
+            if op.startswith("ds_"):
+                pend["lgkm"].append((_regs(ops[0]) if op.startswith("ds_read") else set(), n))
+            elif vmem:
+                pend["vm"].append((_regs(ops[0]) if is_load else set(), n))
+        # more pending operations than any counter can hold (lgkmcnt 15, vmcnt
+        # 63) only arise in a loop without waits: keep the newest, so the walk
+        # ends
+        for cnt in ("lgkm", "vm"):
+            pend[cnt] = pend[cnt][-64:]
+        out = (tuple((frozenset(d), i) for d, i in pend["lgkm"]), tuple((frozenset(d), i) for d, i in pend["vm"]))
+        for nk in succ[k]:
+            work.append((nk, out))
+    return [bad[key] for key in sorted(bad)]
