@@ -128,7 +128,20 @@ constexpr int kQkDepth = 6;            // score A operands read this many k-step
 constexpr int kPvSteps = 16;           // PV operand steps: (ks, column block), 2 MFMAs each
 constexpr int kPvDepth = 4;            // value-read pairs in flight (2 reads per step, lgkmcnt <= 15)
 constexpr int kRotStep = 9;            // PV step after which the RoPE reads of tile t+2 are issued
-constexpr int kRotSlot0 = 26;          // PV slots kRotSlot0 .. +5 rotate and store them
+constexpr int kRotSlot0 = 24;          // PV slots kRotSlot0 .. +6 rotate and store them
+// PV steps from kPostStep0 on keep their odd slot after their second MFMA
+// (the compiler would hoist it above the MFMA, next to the even slot)
+constexpr int kPostStep0 = 12, kPostStep1 = 14;
+// LDS operations a 16-bit cache's wave issues after its RoPE reads (step
+// kRotStep, after its value reads) and before PV slot kRotSlot0 (an even slot:
+// before that step's value reads): the value-read pairs of the steps between
+constexpr int rot_later() {
+  int n = 0;
+  for (int s = kRotStep + 1; s < kRotSlot0 / 2; ++s)
+    if (s + kPvDepth < kPvSteps) n += 2;
+  return n;
+}
+static_assert(kRotSlot0 % 2 == 0 && kRotSlot0 / 2 > kRotStep && rot_later() < 16, "RoPE wait count");
 // FP8 cache: the expansion of tile t+2's staged rows to bf16 runs inside PV(t):
 // rows 0..3 of the wave are read at step kRotStep (after the RoPE reads),
 // everything is waited for at step kExpWaitStep, rows 0..3 are converted and
@@ -145,11 +158,14 @@ constexpr int dma_order(int i) { return (i + 8) % 11; }
 constexpr int kQrAt = 32 - kQkDepth;   // QK step before which the partner-P reads are issued
 constexpr int kTrAt = 36 - kPvDepth;   // QK steps kTrAt.. issue the first kPvDepth PV value-read pairs
 constexpr int kSmSettle = 1;           // softmax slot (two per PV step) that starts softmax(t+1)
-constexpr int kSmExp0 = 8;             // softmax slots kSmExp0 .. +17: the 3-stage exp2 pipeline
+constexpr int kSmPipe0 = 4;            // PV steps kSmPipe0 .. +8 run the exp2 pipeline (one score pair each)
+constexpr int kSmDone = 26;            // softmax slot that takes the summed l
 // the softmax's slots in order: settle / mask, 4 max-tree slots, the running
-// max (kSmSettle + 5), then the exp2 pipeline: overlapping ranges would drop
-// a piece (each slot runs one branch of sm_piece)
-static_assert(kSmExp0 > kSmSettle + 5 && kSmExp0 + 18 < 2 * kPvSteps, "softmax slots in order, inside PV");
+// max (kSmSettle + 5), the exp2 pipeline (its own lead / mid pieces of PV
+// steps kSmPipe0 .. +8, after the running max), then l: overlapping ranges
+// would drop a piece (each slot runs one branch of sm_piece)
+static_assert(2 * kSmPipe0 > kSmSettle + 5 && kSmDone > 2 * (kSmPipe0 + 8) && kSmDone < 2 * kPvSteps,
+              "softmax slots in order, inside PV");
 
 // LDS issue order of one iteration (all reads counted by lgkmcnt):
 //   QK:  [partner flag] A(0..D-1); per step kk: [kk == kQrAt: 2 partner-P
@@ -831,10 +847,10 @@ __device__ inline float rot_k(const RotIn& in, bool second, int e) {
   }
 }
 
-template <typename KT, bool kFp8>
+template <typename KT, bool kFp8, int N = 0>
 __device__ inline void rot_wait(RotIn& in) {
-  if constexpr (kFp8) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(in.k8a), "+v"(in.k8b), "+v"(in.c), "+v"(in.s));
-  else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(in.ka), "+v"(in.kb), "+v"(in.c), "+v"(in.s));
+  if constexpr (kFp8) asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(in.k8a), "+v"(in.k8b), "+v"(in.c), "+v"(in.s) : "n"(N));
+  else asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(in.ka), "+v"(in.kb), "+v"(in.c), "+v"(in.s) : "n"(N));
 }
 
 template <typename KT, bool kFp8>
@@ -1340,8 +1356,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       float mx[5];
       float lmax = -INFINITY;
       uint32_t pw_next[8];  // P(t+1) as bf16/fp16 pairs: word j = positions 2j, 2j+1 of the lane's 16
-      float lpart[4];
-      float sd[16], sx[16];  // s - m and 2^(s - m), one slot apart
+      float lacc;  // l_run plus the P(t+1) pairs summed so far
+      float sd[16], sx[16];  // s - m and 2^(s - m) of the lane's 16 scores
       auto sm_piece = [&](auto step_c) {
         constexpr int step = decltype(step_c)::value;
         if constexpr (step == kSmSettle) {
@@ -1384,34 +1400,44 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
             alpha_pend = alpha;
             resc_pend = __builtin_amdgcn_ballot_w64(!first && alpha != 1.f) != 0;
           }
-        } else if constexpr (step >= kSmExp0 && step < kSmExp0 + 18) {
-          // P = 2^(s - m) <= 2^kRescaleSlack; masked and far-below-max scores
-          // give 0. A 3-stage pipeline over the 16 scores, one per slot:
-          // slot j subtracts for score j, exponentiates score j-1 and packs /
-          // sums the pair ending at j-2, so no op waits on another in its
-          // slot. The empty asm statements hold each result in its slot:
-          // without them the compiler sinks the chain past the PV loop (its
-          // only uses are after it), where no MFMA hides it. l sums P as
-          // rounded to E (the values PV uses), two at a time with v_dot2.
-          constexpr int j = step - kSmExp0;
-          if constexpr (j >= 2 && ((j - 2) & 1)) {
-            constexpr int i = j - 2;
-            typedef E E2 __attribute__((ext_vector_type(2)));
-            const E2 pr = {(E)sx[i - 1], (E)sx[i]};
-            pw_next[i >> 1] = __builtin_bit_cast(uint32_t, pr);
-            lpart[(i >> 1) & 3] = dot2_e(pr, i < 8 ? 0.f : lpart[(i >> 1) & 3]);
-            asm volatile("" : "+v"(pw_next[i >> 1]), "+v"(lpart[(i >> 1) & 3]));
-          }
-          if constexpr (j >= 1 && j <= 16) {
-            sx[j - 1] = __builtin_amdgcn_exp2f(sd[j - 1]);
-            asm volatile("" : "+v"(sx[j - 1]));
-          }
-          if constexpr (j < 16) {
-            sd[j] = s_next[j] - m_run;
-            asm volatile("" : "+v"(sd[j]));
-          }
-        } else if constexpr (step == kSmExp0 + 18) {
-          if (sm) l_run += (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
+        } else if constexpr (step == kSmDone) {
+          if (sm) l_run = lacc;
+        }
+      };
+      // The exp2 pipeline, one pair of the lane's 16 scores per PV step k =
+      // step - kSmPipe0: P = 2^(s - m) <= 2^kRescaleSlack (masked and
+      // far-below-max scores give 0); l sums P as rounded to E (the values PV
+      // uses) with v_dot2. The lead piece runs after the step's value-read
+      // wait, before its first MFMA (while the previous step's second MFMA
+      // runs): s - m of pair k and the packing of pair k-1. The mid piece runs
+      // between the step's two MFMAs: 2^(s - m) of pair k and the sum of pair
+      // k-1. The empty asm statements hold each result in its piece: without
+      // them the compiler sinks the chain past the PV loop (its only uses are
+      // after it), where no MFMA hides it.
+      typedef E E2 __attribute__((ext_vector_type(2)));
+      auto sm_lead = [&](auto step_c) {
+        constexpr int k = decltype(step_c)::value - kSmPipe0;
+        if constexpr (k >= 0 && k <= 7) {
+          sd[2 * k] = s_next[2 * k] - m_run;
+          sd[2 * k + 1] = s_next[2 * k + 1] - m_run;
+          asm volatile("" : "+v"(sd[2 * k]), "+v"(sd[2 * k + 1]));
+        }
+        if constexpr (k >= 1 && k <= 8) {
+          const E2 pr = {(E)sx[2 * k - 2], (E)sx[2 * k - 1]};
+          pw_next[k - 1] = __builtin_bit_cast(uint32_t, pr);
+          asm volatile("" : "+v"(pw_next[k - 1]));
+        }
+      };
+      auto sm_mid = [&](auto step_c) {
+        constexpr int k = decltype(step_c)::value - kSmPipe0;
+        if constexpr (k >= 1 && k <= 8) {
+          lacc = dot2_e(__builtin_bit_cast(E2, pw_next[k - 1]), k == 1 ? l_run : lacc);
+          asm volatile("" : "+v"(lacc));
+        }
+        if constexpr (k >= 0 && k <= 7) {
+          sx[2 * k] = __builtin_amdgcn_exp2f(sd[2 * k]);
+          sx[2 * k + 1] = __builtin_amdgcn_exp2f(sd[2 * k + 1]);
+          asm volatile("" : "+v"(sx[2 * k]), "+v"(sx[2 * k + 1]));
         }
       };
 
@@ -1456,13 +1482,13 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       RotIn rot;
       float rot_k0[4], rot_k1[4], rot_a[4], rot_b[4];
       auto rot_piece = [&](auto slot_c) {
-        // slot r: widen pair e = 2r, 2r+1 (r < 2); products of pair r-1,
-        // sums of pair r-2; the last slot stores
+        // slot r: widen pairs e = 2r, 2r+1 (r < 2); products and sums of
+        // pair r-2 (r = 2..5); store (r = 6)
         constexpr int r = decltype(slot_c)::value - kRotSlot0;
         if constexpr (r == 0) {
           // FP8 cache: step kExpWaitStep has waited for the RoPE reads
           if constexpr (kFp8) asm volatile("" : "+v"(rot.k8a), "+v"(rot.k8b), "+v"(rot.c), "+v"(rot.s));
-          else rot_wait<KT, kFp8>(rot);
+          else rot_wait<KT, kFp8, rot_later()>(rot);
         }
         if constexpr (r >= 0 && r < 2) {
 #pragma unroll
@@ -1478,7 +1504,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           rot_b[e] = rot_k0[e] * rot.s[e] + rot_k1[e] * rot.c[e];
           asm volatile("" : "+v"(rot_a[e]), "+v"(rot_b[e]));
         }
-        if constexpr (r == 5) rot_store<KT>(L, rot, rot_a, rot_b);
+        if constexpr (r == 6) rot_store<KT>(L, rot, rot_a, rot_b);
       };
       static_for<kPvSteps>([&](auto step_c) {
         constexpr int step = decltype(step_c)::value;
@@ -1501,6 +1527,12 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
           bv[4 + e] = bc.x1[e];
         }
         const vec bvec = __builtin_bit_cast(vec, bv);
+        // the lead piece stays after the wait: hoisted above it, as the
+        // compiler would, it leaves the MFMA right behind the wait, with a
+        // wait state between them
+        __builtin_amdgcn_sched_barrier(0);
+        sm_lead(step_c);
+        __builtin_amdgcn_sched_barrier(0);
         // A wave issues in order and an MFMA waits for the previous one to
         // leave the pipe, so VALU work placed between the two MFMAs runs while
         // the first executes; placed after both it would wait for the second
@@ -1508,11 +1540,13 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         O_::mma_a(acc[cb], bvec, p_cur[ks]);
         __builtin_amdgcn_sched_barrier(0);
         sm_piece(std::integral_constant<int, 2 * step>());
+        sm_mid(step_c);
         rot_piece(std::integral_constant<int, 2 * step>());
         exp_piece(std::integral_constant<int, 2 * step>());
         __builtin_amdgcn_sched_barrier(0);
         O_::mma_a(acc[8 + cb], bvec, pp[ks]);
         if constexpr (step + kPvDepth < kPvSteps) b_issue(bc, std::integral_constant<int, step + kPvDepth>());
+        if constexpr (step >= kPostStep0 && step <= kPostStep1) __builtin_amdgcn_sched_barrier(0);
         if constexpr (step == kRotStep) {
           // this wave's k_rope / cos / sin copies of tile t+2 have landed (an
           // fp8 tile's k_rope parts come with every row copy)
@@ -1536,9 +1570,10 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         p_cur[1] = __builtin_bit_cast(vec, u32x4{pw_next[4], pw_next[5], pw_next[6], pw_next[7]});
         lds_st(L, ptab, p_cur[0]);
         lds_st(L, ptab + 1024, p_cur[1]);
+        // lanes 0..31 store the alpha of head lane, every lane from 32 on the
+        // flag word (alpha slot 32) with the same value: one store, no exec mask
         const uint32_t natab = kAtabOff + npar * kAtabPar + wave * kAtabWave;
-        if (lane < 32) lds_st(L, natab + 4 * lane, alpha_pend);
-        if (lane == 0) lds_st(L, natab + 128, resc_pend ? 1.f : 0.f);
+        lds_st(L, natab + 4 * min(lane, 32), lane < 32 ? alpha_pend : (resc_pend ? 1.f : 0.f));
       }
 #ifdef LA_PHASE_STAMPS
       LA_TSTAMP(tt3);
