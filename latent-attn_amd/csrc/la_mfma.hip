@@ -521,16 +521,6 @@ __device__ inline float max3f(float a, float b, float c) {
   asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
   return r;
 }
-// c + p.x + p.y for a pair of 16-bit P values (v_dot2 with (1, 1))
-__device__ inline float dot2_e(__bf16 __attribute__((ext_vector_type(2))) p, float c) {
-  const __bf16 __attribute__((ext_vector_type(2))) one = {(__bf16)1.f, (__bf16)1.f};
-  return __builtin_amdgcn_fdot2_f32_bf16(p, one, c, false);
-}
-__device__ inline float dot2_e(_Float16 __attribute__((ext_vector_type(2))) p, float c) {
-  const _Float16 __attribute__((ext_vector_type(2))) one = {(_Float16)1.f, (_Float16)1.f};
-  return __builtin_amdgcn_fdot2(p, one, c, false);
-}
-
 // The partner's rescale flag and the first six score operands of a QK phase,
 // in one asm statement that waits for the flag (issued first) before it
 // ends. A value read by one asm and waited for by a later one can be copied by
@@ -1356,7 +1346,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       float mx[5];
       float lmax = -INFINITY;
       uint32_t pw_next[8];  // P(t+1) as bf16/fp16 pairs: word j = positions 2j, 2j+1 of the lane's 16
-      float lacc;  // l_run plus the P(t+1) pairs summed so far
+      float lacc;  // l_run plus the P(t+1) values summed so far
       float sd[16], sx[16];  // s - m and 2^(s - m) of the lane's 16 scores
       auto sm_piece = [&](auto step_c) {
         constexpr int step = decltype(step_c)::value;
@@ -1406,14 +1396,16 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
       };
       // The exp2 pipeline, one pair of the lane's 16 scores per PV step k =
       // step - kSmPipe0: P = 2^(s - m) <= 2^kRescaleSlack (masked and
-      // far-below-max scores give 0); l sums P as rounded to E (the values PV
-      // uses) with v_dot2. The lead piece runs after the step's value-read
+      // far-below-max scores give 0); l sums P in fp32 with v_add (a v_dot2
+      // over the packed pair would wait for the MFMA in flight, like every
+      // dot instruction). The lead piece runs after the step's value-read
       // wait, before its first MFMA (while the previous step's second MFMA
-      // runs): s - m of pair k and the packing of pair k-1. The mid piece runs
-      // between the step's two MFMAs: 2^(s - m) of pair k and the sum of pair
-      // k-1. The empty asm statements hold each result in its piece: without
-      // them the compiler sinks the chain past the PV loop (its only uses are
-      // after it), where no MFMA hides it.
+      // runs): s - m of pair k, the packing of pair k-1 and the sum of its
+      // first value. The mid piece runs between the step's two MFMAs: the sum
+      // of pair k-1's second value and 2^(s - m) of pair k. The empty asm
+      // statements hold each result in its piece: without them the compiler
+      // sinks the chain past the PV loop (its only uses are after it), where
+      // no MFMA hides it.
       typedef E E2 __attribute__((ext_vector_type(2)));
       auto sm_lead = [&](auto step_c) {
         constexpr int k = decltype(step_c)::value - kSmPipe0;
@@ -1425,13 +1417,14 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeProblem p, 
         if constexpr (k >= 1 && k <= 8) {
           const E2 pr = {(E)sx[2 * k - 2], (E)sx[2 * k - 1]};
           pw_next[k - 1] = __builtin_bit_cast(uint32_t, pr);
-          asm volatile("" : "+v"(pw_next[k - 1]));
+          lacc = (k == 1 ? l_run : lacc) + sx[2 * k - 2];
+          asm volatile("" : "+v"(pw_next[k - 1]), "+v"(lacc));
         }
       };
       auto sm_mid = [&](auto step_c) {
         constexpr int k = decltype(step_c)::value - kSmPipe0;
         if constexpr (k >= 1 && k <= 8) {
-          lacc = dot2_e(__builtin_bit_cast(E2, pw_next[k - 1]), k == 1 ? l_run : lacc);
+          lacc += sx[2 * k - 1];
           asm volatile("" : "+v"(lacc));
         }
         if constexpr (k >= 0 && k <= 7) {
